@@ -1,0 +1,249 @@
+/*
+ * seqattn_hip.h - C ABI of the MI355X (gfx950) streamed exact-attention library.
+ *
+ * The library is libseqattn_hip.so, built from stream-attn_amd/csrc/.  Every entry
+ * point takes plain device or pinned-host pointers, element strides and sizes;
+ * no C++ type or exception crosses this boundary.  The caller owns all memory:
+ * the library never allocates or frees caller buffers.  A pipeline object owns
+ * only its own HIP streams and events.
+ *
+ * Return codes: 0 on success, a positive hipError_t when the HIP runtime
+ * failed, or one of the negative SA_ERR_* codes when an argument was rejected.
+ * sa_last_error() returns a message describing the most recent failure on the
+ * calling thread.
+ *
+ * Tensor layouts follow the reference: packed [tokens, heads, head_dim] with
+ * the head_dim stride equal to 1; every other stride is passed in elements.
+ */
+#ifndef SEQATTN_HIP_H
+#define SEQATTN_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SA_ABI_VERSION 1
+
+/* dtype codes for Q/K/V/output element types */
+#define SA_DTYPE_BF16 0
+#define SA_DTYPE_FP16 1
+
+/* sa_update_attention_state flags */
+#define SA_FLAG_CAUSAL 1
+#define SA_FLAG_INITIALIZE 2
+
+/* negative error codes (positive codes are hipError_t values) */
+#define SA_ERR_INVALID_ARGUMENT (-1)
+#define SA_ERR_UNSUPPORTED_DTYPE (-2)
+#define SA_ERR_UNSUPPORTED_HEAD_DIM (-3)
+#define SA_ERR_BAD_STATE (-4)
+
+/* ABI version of the loaded library; equals SA_ABI_VERSION when it matches
+ * this header. */
+int32_t sa_abi_version(void);
+
+/* Message for the most recent failure on the calling thread ("" if none). */
+const char* sa_last_error(void);
+
+/*
+ * One K/V chunk's online-softmax update of the FP32 state (m, l, acc) of a
+ * resident query block.
+ *
+ * Replaces update_attention_state (reference src/seqattn_core/kernels/streaming.py:205-271),
+ * which launches _streaming_attention_update_kernel (same file, lines 19-156).
+ *
+ *   q    [q_tokens, q_heads, head_dim]      bf16/fp16, strides (stride_qt, stride_qh, 1)
+ *   k, v [kv_tokens, kv_heads, head_dim]    same dtype, strides (stride_kt, stride_kh, 1) / (stride_vt, stride_vh, 1)
+ *   running_max, running_sum [q_tokens, q_heads]  fp32, shared strides (stride_st, stride_sh)
+ *   accumulator [q_tokens, q_heads, head_dim]     fp32, strides (stride_at, stride_ah, 1)
+ *
+ * Logits are q.k * softmax_scale * log2(e) (base-2 domain).  With
+ * SA_FLAG_CAUSAL, key kv_local_offset + j is visible to query q_local_offset + i
+ * iff kv_local_offset + j <= q_local_offset + i + causal_shift.  With
+ * SA_FLAG_INITIALIZE the state starts at m = -inf, l = 0, acc = 0 instead of
+ * being read.  q_heads must be a multiple of kv_heads (query head h reads K/V
+ * head h / (q_heads / kv_heads)).  head_dim is a multiple of 8 in [16, 256].
+ * The launch is asynchronous on `stream` (a hipStream_t, NULL = default stream).
+ */
+int32_t sa_update_attention_state(
+    const void* q, const void* k, const void* v,
+    float* running_max, float* running_sum, float* accumulator,
+    int64_t stride_qt, int64_t stride_qh,
+    int64_t stride_kt, int64_t stride_kh,
+    int64_t stride_vt, int64_t stride_vh,
+    int64_t stride_st, int64_t stride_sh,
+    int64_t stride_at, int64_t stride_ah,
+    int32_t q_tokens, int32_t kv_tokens,
+    int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+    int32_t q_local_offset, int32_t kv_local_offset, int32_t causal_shift,
+    double softmax_scale, int32_t flags, int32_t dtype,
+    void* stream);
+
+/*
+ * out = acc / l where l > 0, else 0, cast to dtype; optionally
+ * lse = ln(sum exp(logits)) = (m + log2 l) * ln 2 (natural log), -inf where l == 0.
+ *
+ * Replaces finalize_attention (reference src/seqattn_core/kernels/streaming.py:345-371),
+ * which launches _finalize_attention_kernel (lines 158-202); the LSE output has
+ * no counterpart in the reference.
+ *
+ *   accumulator [q_tokens, q_heads, head_dim] fp32, strides (stride_at, stride_ah, 1)
+ *   running_max, running_sum [q_tokens, q_heads] fp32, strides (stride_st, stride_sh)
+ *   out [q_tokens, q_heads, head_dim] dtype, strides (stride_ot, stride_oh, 1)
+ *   lse (may be NULL) fp32, element (h, t) at lse[h * lse_stride_h + lse_token_offset + t]
+ *
+ * running_max may be NULL when lse is NULL.  `out` may alias the query buffer
+ * that fed the update (device-consumer mode): this kernel reads only the state.
+ */
+int32_t sa_finalize_attention(
+    const float* accumulator, const float* running_max, const float* running_sum,
+    void* out, float* lse,
+    int64_t stride_at, int64_t stride_ah,
+    int64_t stride_st, int64_t stride_sh,
+    int64_t stride_ot, int64_t stride_oh,
+    int64_t lse_stride_h, int64_t lse_token_offset,
+    int32_t q_tokens, int32_t q_heads, int32_t head_dim, int32_t dtype,
+    void* stream);
+
+/* ------------------------------------------------------------------------ */
+/* Transfer pipeline: pinned host Q/K/V -> HBM workspace -> pinned host out. */
+/* ------------------------------------------------------------------------ */
+
+typedef struct sa_pipeline sa_pipeline;
+
+typedef struct sa_pipeline_stats {
+    int64_t h2d_bytes;
+    int64_t d2h_bytes;
+    int64_t q_chunks;
+    int64_t kv_tiles;
+    int64_t max_resident_q_tokens;
+} sa_pipeline_stats;
+
+/*
+ * Bind a pipeline to caller-owned device workspace buffers (the layout of
+ * CudaWorkspace, reference src/seqattn_core/streaming/workspace.py:8-50) and
+ * its two copy streams (H2D, D2H), and create its ready/free events.
+ *
+ *   q_buffer      [q_chunk_tokens, q_heads, head_dim] dtype
+ *   k_slots[i], v_slots[i]  [kv_chunk_tokens, kv_heads, head_dim] dtype, i < num_kv_buffers (1..3)
+ *   running_max, running_sum [q_chunk_tokens, q_heads] fp32
+ *   accumulator   [q_chunk_tokens, q_heads, head_dim] fp32
+ *   out_slots     NULL (device-consumer mode: no raw output buffers) or
+ *                 num_output_buffers pointers to [q_chunk_tokens, q_heads, head_dim] dtype
+ *   num_output_buffers  1..2: output ready/free event pairs (and slots when out_slots != NULL)
+ *   h2d_stream, d2h_stream  caller hipStream_t handles for the copies, or NULL
+ *                 for streams the pipeline creates (default priority) and
+ *                 destroys with itself.  Caller streams must outlive the
+ *                 pipeline; a caller whose allocator tracks stream uses of
+ *                 its buffers (torch record_stream) must pass its own streams.
+ * All buffers are contiguous.
+ */
+int32_t sa_pipeline_create(
+    sa_pipeline** out_pipeline, int32_t device,
+    void* q_buffer, void* const* k_slots, void* const* v_slots, int32_t num_kv_buffers,
+    float* running_max, float* running_sum, float* accumulator,
+    void* const* out_slots, int32_t num_output_buffers,
+    int32_t q_chunk_tokens, int32_t kv_chunk_tokens,
+    int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t dtype,
+    void* h2d_stream, void* d2h_stream);
+
+/* Wait for all pending copies of the pipeline, then release its events and the streams it created. */
+int32_t sa_pipeline_destroy(sa_pipeline* pipeline);
+
+/*
+ * Whole tensor-mode schedule with host output (reference
+ * src/seqattn_core/streaming/executor.py:18-188 without output_transform):
+ * for each segment, for each Q super-block: Q H2D on the H2D stream, then per
+ * K/V chunk an H2D into the next ring slot (fenced by that slot's free event)
+ * and an update launch on compute_stream (fenced by the slot's ready event),
+ * then finalize into an output slot and D2H into out_host on the D2H stream.
+ * Returns after the D2H stream has drained.
+ *
+ *   q_host/k_host/v_host/out_host: contiguous pinned host [tokens, heads, head_dim] dtype
+ *   cu_seqlens_q/k: num_segments + 1 host int64 boundaries
+ *   lse (may be NULL): device fp32 [q_heads, lse_stride_h >= total_q_tokens]
+ *   stats (may be NULL): counters are ADDED to it
+ */
+int32_t sa_pipeline_run(
+    sa_pipeline* pipeline,
+    const void* q_host, const void* k_host, const void* v_host, void* out_host,
+    float* lse, int64_t lse_stride_h,
+    const int64_t* cu_seqlens_q, const int64_t* cu_seqlens_k, int32_t num_segments,
+    double softmax_scale, int32_t causal,
+    void* compute_stream, sa_pipeline_stats* stats);
+
+/*
+ * Step interface used by device-consumer mode (reference executor.py:44-186
+ * with output_transform): the caller runs one Q super-block at a time and may
+ * consume the finalized device tile between finalize and D2H.  sa_pipeline_run
+ * is these steps in a loop.
+ *
+ * sa_pipeline_load_q: H2D of q_tokens rows from q_host (already offset to the
+ * super-block start) into q_buffer on the H2D stream, after the Q-free event
+ * of the previous super-block; compute_stream then waits for the copy.
+ */
+int32_t sa_pipeline_load_q(sa_pipeline* pipeline, const void* q_host, int32_t q_tokens,
+                           void* compute_stream, sa_pipeline_stats* stats);
+
+/* Stream one segment's K/V (k_host/v_host offset to the segment start,
+ * k_length rows) through the ring in kv_chunk_tokens chunks and apply every
+ * chunk to the resident Q block (executor.py:68-123). */
+int32_t sa_pipeline_stream_kv(sa_pipeline* pipeline, const void* k_host, const void* v_host,
+                              int32_t k_length, int32_t q_tokens, int32_t q_local_offset,
+                              int32_t causal_shift, double softmax_scale, int32_t causal,
+                              void* compute_stream, sa_pipeline_stats* stats);
+
+/*
+ * Finalize the resident state on compute_stream (executor.py:125-142).
+ * slot >= 0: into output slot `slot`; the Q-free event is recorded first (the
+ * next Q H2D may start) and finalize waits for the slot's previous D2H.
+ * slot == -1: into q_buffer itself (device-consumer Q reuse); Q stays held
+ * until sa_pipeline_d2h(release_q=1) or sa_pipeline_release_q.
+ * lse as in sa_finalize_attention (NULL for none).
+ */
+int32_t sa_pipeline_finalize(sa_pipeline* pipeline, int32_t slot, int32_t q_tokens,
+                             float* lse, int64_t lse_stride_h, int64_t lse_token_offset,
+                             void* compute_stream);
+
+/*
+ * Finalize the resident state straight into a caller device buffer `dest`
+ * with strides (stride_ot, stride_oh, 1) on compute_stream: the output stays
+ * in HBM and no D2H is issued.  The Q-free event is recorded first.
+ */
+int32_t sa_pipeline_finalize_into(sa_pipeline* pipeline, void* dest, int64_t stride_ot,
+                                  int64_t stride_oh, int32_t q_tokens, float* lse,
+                                  int64_t lse_stride_h, int64_t lse_token_offset,
+                                  void* compute_stream);
+
+/* Record the Q-free event on compute_stream (a consumer produced a new tensor
+ * and no longer needs the Q buffer, executor.py:170-172). */
+int32_t sa_pipeline_release_q(sa_pipeline* pipeline, void* compute_stream);
+
+/*
+ * D2H of `bytes` from device `src` to pinned host `dst_host` on the D2H stream
+ * after everything enqueued on compute_stream so far (executor.py:173-184).
+ * Output events of `event_slot` (0 <= event_slot < num_output_buffers) fence
+ * the next finalize into that slot; release_q != 0 (src lives in q_buffer)
+ * records the Q-free event on the D2H stream.
+ */
+int32_t sa_pipeline_d2h(sa_pipeline* pipeline, void* dst_host, const void* src, int64_t bytes,
+                        int32_t event_slot, int32_t release_q, void* compute_stream,
+                        sa_pipeline_stats* stats);
+
+/* Block until the D2H stream has drained. */
+int32_t sa_pipeline_synchronize(sa_pipeline* pipeline);
+
+/* hipStream_t of the pipeline's H2D (which == 0) or D2H (which == 1) copy stream. */
+void* sa_pipeline_stream(sa_pipeline* pipeline, int32_t which);
+
+/* Device pointers: output slot `index` (NULL without slots) and the Q buffer. */
+void* sa_pipeline_output_slot(sa_pipeline* pipeline, int32_t index);
+void* sa_pipeline_q_buffer(sa_pipeline* pipeline);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SEQATTN_HIP_H */

@@ -1,0 +1,234 @@
+"""CPU oracle of the streamed exact-attention path.  TEST INFRASTRUCTURE ONLY.
+
+This module is the checker for the GPU path: only ``tests/``,
+``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+use it, and never as the thing that is measured or shipped.  The product
+package (``stream-attn_amd/seqattn``) never imports it.
+
+Every function is a numpy restatement of the reference algorithm; each cites
+the reference file:line it follows.  Parity pins (see tests/test_oracle.py):
+
+* ``chunked_attention`` (O and LSE) against a dense float64 closed form
+  ``softmax(QK^T s)V`` / ``logsumexp(QK^T s)``, against the reference test's
+  known answers (segment isolation 0 / 10, "queries but no keys"), against a
+  brute-force per-row float64 loop on tiny inputs, and across chunk sizes
+  (chunking must not change the result beyond fp32 rounding).
+* ``chunked_attention_rows`` equals ``chunked_attention`` on the same rows.
+* ``seeded_normal_chunks`` reproduces torch's generator stream exactly (it
+  calls torch's CPU generator, the same calls the reference's benchmark
+  makes) and is checked element-for-element against a direct torch call.
+"""
+
+from __future__ import annotations
+
+import math
+
+import numpy as np
+
+
+def segment_bounds(cu: np.ndarray | list[int], total: int, name: str) -> list[int]:
+    """Validated cumulative bounds (reference src/seqattn_core/validation.py:18-26)."""
+    bounds = [int(x) for x in np.asarray(cu).reshape(-1).tolist()]
+    if len(bounds) < 2:
+        raise ValueError(f"{name} must be a one-dimensional CPU tensor")
+    if bounds[0] != 0 or bounds[-1] != total:
+        raise ValueError(f"{name} must span [0, {total}], got {bounds}")
+    if any(b < a for a, b in zip(bounds[:-1], bounds[1:])):
+        raise ValueError(f"{name} must be non-decreasing")
+    return bounds
+
+
+def _validate(q, k, v, cu_q, cu_k):
+    """Shape/segment checks of reference validation.py:6-47."""
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("q, k, and v must use packed [tokens, heads, head_dim] layout")
+    if k.shape != v.shape:
+        raise ValueError("k and v must have identical shapes")
+    if q.shape[2] != k.shape[2]:
+        raise ValueError("q and k/v must use the same head_dim")
+    if q.shape[1] % k.shape[1]:
+        raise ValueError("the number of query heads must be divisible by the number of KV heads")
+    qb = segment_bounds(cu_q, q.shape[0], "cu_seqlens_q")
+    kb = segment_bounds(cu_k, k.shape[0], "cu_seqlens_k")
+    if len(qb) != len(kb):
+        raise ValueError("cu_seqlens_q and cu_seqlens_k must describe the same batch size")
+    for i in range(len(qb) - 1):
+        if qb[i + 1] > qb[i] and kb[i + 1] == kb[i]:
+            raise ValueError(f"sequence {i} has queries but no keys")
+    return qb, kb
+
+
+def chunked_attention(
+    q: np.ndarray,
+    k: np.ndarray,
+    v: np.ndarray,
+    cu_q,
+    cu_k,
+    *,
+    q_chunk_tokens: int,
+    kv_chunk_tokens: int,
+    softmax_scale: float | None = None,
+    causal: bool = False,
+    rows: np.ndarray | None = None,
+) -> tuple[np.ndarray, np.ndarray]:
+    """FP32 online-softmax attention; returns (O [T, H, D] fp32, LSE [H, T] fp32).
+
+    Follows streaming_attention_reference (reference src/seqattn_core/reference.py:11-117):
+    per segment (L44), per Q tile of q_chunk_tokens (L50), state m=-inf, l=0,
+    o=0 (L53-61); per K/V tile of kv_chunk_tokens (L68): GQA by repeating K/V
+    heads (L73-75), s = q k^T * scale (L78), bottom-right causal mask
+    k_pos <= q_pos + (Lk - Lq) (L79-88), m' = max(m, rowmax s), alpha =
+    exp(m - m') where m' is finite else 1, p = exp(s - m') where s is finite
+    else 0, l = l*alpha + sum p, o = o*alpha + p v (L90-107); out = o / l
+    where l > 0 else 0 (L109-113).  LSE (absent from the reference) is
+    m + ln(l), -inf where l == 0.
+
+    ``rows`` (optional, sorted global query indices) restricts the work to
+    those query rows: each Q tile is intersected with them, which leaves the
+    per-row recurrence unchanged.  Returned arrays are full-size; rows not
+    computed are NaN.
+    """
+    q = np.asarray(q)
+    k = np.asarray(k)
+    v = np.asarray(v)
+    qb, kb = _validate(q, k, v, cu_q, cu_k)
+    if q_chunk_tokens <= 0 or kv_chunk_tokens <= 0:
+        raise ValueError("q_chunk_tokens and kv_chunk_tokens must be positive")
+    tokens, heads, head_dim = q.shape
+    group = heads // k.shape[1]
+    scale = head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
+    out = np.full((tokens, heads, head_dim), np.nan, dtype=np.float32)
+    lse = np.full((heads, tokens), np.nan, dtype=np.float32)
+    row_mask = None
+    if rows is not None:
+        row_mask = np.zeros(tokens, dtype=bool)
+        row_mask[np.asarray(rows, dtype=np.int64)] = True
+
+    for q_start, q_stop, k_start, k_stop in zip(qb[:-1], qb[1:], kb[:-1], kb[1:]):
+        causal_shift = (k_stop - k_start) - (q_stop - q_start)
+        for tile_start in range(q_start, q_stop, q_chunk_tokens):
+            tile_stop = min(tile_start + q_chunk_tokens, q_stop)
+            idx = np.arange(tile_start, tile_stop)
+            if row_mask is not None:
+                idx = idx[row_mask[tile_start:tile_stop]]
+                if idx.size == 0:
+                    continue
+            qt = np.ascontiguousarray(q[idx].astype(np.float32).transpose(1, 0, 2))  # [H, n, D]
+            n = idx.size
+            m = np.full((heads, n), -np.inf, dtype=np.float32)
+            l = np.zeros((heads, n), dtype=np.float32)
+            o = np.zeros((heads, n, head_dim), dtype=np.float32)
+            q_pos = idx - q_start
+            for kv_start in range(k_start, k_stop, kv_chunk_tokens):
+                kv_stop = min(kv_start + kv_chunk_tokens, k_stop)
+                kt = k[kv_start:kv_stop].astype(np.float32)
+                vt = v[kv_start:kv_stop].astype(np.float32)
+                if group != 1:
+                    kt = np.repeat(kt, group, axis=1)
+                    vt = np.repeat(vt, group, axis=1)
+                kt = kt.transpose(1, 0, 2)  # [H, n_k, D]
+                vt = vt.transpose(1, 0, 2)
+                s = np.matmul(qt, kt.transpose(0, 2, 1)) * np.float32(scale)
+                if causal:
+                    k_pos = np.arange(kv_start - k_start, kv_stop - k_start)
+                    visible = k_pos[None, :] <= (q_pos[:, None] + causal_shift)
+                    s = np.where(visible[None], s, -np.inf).astype(np.float32)
+                tile_max = s.max(axis=-1)
+                merged = np.maximum(m, tile_max)
+                finite = np.isfinite(merged)
+                with np.errstate(invalid="ignore"):
+                    alpha = np.where(finite, np.exp(m - merged), np.float32(1.0)).astype(np.float32)
+                    p = np.where(np.isfinite(s), np.exp(s - merged[..., None]), np.float32(0.0))
+                p = p.astype(np.float32)
+                l = l * alpha + p.sum(axis=-1, dtype=np.float32)
+                o = o * alpha[..., None] + np.matmul(p, vt)
+                m = np.where(finite, merged, m)
+            positive = l > 0
+            with np.errstate(divide="ignore", invalid="ignore"):
+                normalized = np.where(positive[..., None], o / l[..., None], np.float32(0.0))
+                lse_tile = np.where(positive, m + np.log(l), -np.inf)
+            out[idx] = normalized.transpose(1, 0, 2)
+            lse[:, idx] = lse_tile
+    return out, lse
+
+
+def dense_attention_f64(q, k, v, cu_q, cu_k, *, softmax_scale=None, causal=False, rows=None):
+    """Closed form softmax(QK^T s)V and logsumexp(QK^T s) in float64.
+
+    The oracle's pin: an independent, unchunked computation of the same
+    quantity (reference tests/test_reference.py:13-38 uses the same closed
+    form to pin its chunked reference).
+    """
+    q = np.asarray(q, dtype=np.float64)
+    k = np.asarray(k, dtype=np.float64)
+    v = np.asarray(v, dtype=np.float64)
+    qb, kb = _validate(q, k, v, cu_q, cu_k)
+    tokens, heads, head_dim = q.shape
+    group = heads // k.shape[1]
+    scale = head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
+    out = np.full((tokens, heads, head_dim), np.nan)
+    lse = np.full((heads, tokens), np.nan)
+    selected = None if rows is None else set(int(r) for r in rows)
+    for qs, qe, ks, ke in zip(qb[:-1], qb[1:], kb[:-1], kb[1:]):
+        idx = np.arange(qs, qe)
+        if selected is not None:
+            idx = np.array([i for i in idx if i in selected], dtype=np.int64)
+        if idx.size == 0:
+            continue
+        kk = np.repeat(k[ks:ke], group, axis=1).transpose(1, 0, 2)
+        vv = np.repeat(v[ks:ke], group, axis=1).transpose(1, 0, 2)
+        s = np.matmul(q[idx].transpose(1, 0, 2), kk.transpose(0, 2, 1)) * scale
+        if causal:
+            shift = (ke - ks) - (qe - qs)
+            visible = np.arange(ke - ks)[None, :] <= (idx - qs)[:, None] + shift
+            s = np.where(visible[None], s, -np.inf)
+        mx = s.max(axis=-1, keepdims=True)
+        safe = np.where(np.isfinite(mx), mx, 0.0)
+        e = np.exp(s - safe)
+        total = e.sum(axis=-1, keepdims=True)
+        with np.errstate(divide="ignore", invalid="ignore"):
+            o = np.where(total > 0, np.matmul(e, vv) / total, 0.0)
+            ls = np.where(total[..., 0] > 0, safe[..., 0] + np.log(total[..., 0]), -np.inf)
+        out[idx] = o.transpose(1, 0, 2)
+        lse[:, idx] = ls
+    return out, lse
+
+
+def brute_force_row(q_row, k_seg, v_seg, *, scale, visible_keys=None):
+    """One query row of one head by explicit loops in float64 (tiny inputs only)."""
+    n_keys = k_seg.shape[0] if visible_keys is None else visible_keys
+    if n_keys <= 0:
+        return np.zeros(k_seg.shape[1]), -math.inf
+    logits = [float(np.dot(q_row, k_seg[j])) * scale for j in range(n_keys)]
+    top = max(logits)
+    weights = [math.exp(x - top) for x in logits]
+    total = sum(weights)
+    o = sum(w * v_seg[j] for j, w in enumerate(weights)) / total
+    return o, top + math.log(total)
+
+
+def seeded_normal_chunks(tokens: int, heads: int, head_dim: int, *, seed: int, tensor_index: int,
+                         chunk_tokens: int = 4096, dtype=None):
+    """Input tensor as the reference benchmark fills it (benchmarking/common.py:47-73).
+
+    Chunk c of tensor t is ``normal_`` from a CPU generator seeded with
+    ``seed + t * 1_000_003 + c``.  Returns a torch tensor (the generator
+    stream is torch's, so the values are bit-identical to the reference's).
+    """
+    import torch
+
+    dtype = torch.bfloat16 if dtype is None else dtype
+    out = torch.empty((tokens, heads, head_dim), dtype=dtype)
+    for c, start in enumerate(range(0, tokens, chunk_tokens)):
+        g = torch.Generator(device="cpu").manual_seed(seed + tensor_index * 1_000_003 + c)
+        out[start : min(start + chunk_tokens, tokens)].normal_(generator=g)
+    return out
+
+
+__all__ = [
+    "brute_force_row",
+    "chunked_attention",
+    "dense_attention_f64",
+    "seeded_normal_chunks",
+    "segment_bounds",
+]

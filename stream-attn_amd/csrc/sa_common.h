@@ -1,0 +1,66 @@
+// Shared host-side helpers of libseqattn_hip: thread-local error text and
+// HIP status propagation.  No exception crosses the C ABI: every failure is a
+// return code plus a message readable through sa_last_error().
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "seqattn_hip.h"
+
+namespace sa {
+
+void set_error(const char* fmt, ...);
+void clear_error();
+
+// Converts a hipError_t into the ABI convention (0 or a positive code) and
+// records a message naming the failing call.
+int32_t hip_status(hipError_t err, const char* what);
+
+// Makes `device` current for the lifetime of the guard and restores the
+// caller's device afterwards (torch tracks its own current device per thread).
+class DeviceGuard {
+ public:
+  explicit DeviceGuard(int device) {
+    hipGetDevice(&previous_);
+    if (previous_ != device) {
+      hipSetDevice(device);
+      changed_ = true;
+    }
+  }
+  ~DeviceGuard() {
+    if (changed_) hipSetDevice(previous_);
+  }
+  DeviceGuard(const DeviceGuard&) = delete;
+  DeviceGuard& operator=(const DeviceGuard&) = delete;
+
+ private:
+  int previous_ = 0;
+  bool changed_ = false;
+};
+
+}  // namespace sa
+
+#define SA_HIP_RETURN(call)                                  \
+  do {                                                       \
+    hipError_t sa_err_ = (call);                             \
+    if (sa_err_ != hipSuccess) return sa::hip_status(sa_err_, #call); \
+  } while (0)
+
+// Kernel entry points shared between the kernel and pipeline translation units.
+namespace sa {
+int32_t launch_update(const void* q, const void* k, const void* v, float* m, float* l, float* acc,
+                      int64_t sq_t, int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t,
+                      int64_t sv_h, int64_t ss_t, int64_t ss_h, int64_t sa_t, int64_t sa_h,
+                      int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
+                      int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
+                      int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
+                      hipStream_t stream);
+int32_t launch_finalize(const float* acc, const float* m, const float* l, void* out, float* lse,
+                        int64_t sa_t, int64_t sa_h, int64_t ss_t, int64_t ss_h, int64_t so_t,
+                        int64_t so_h, int64_t lse_sh, int64_t lse_off, int32_t q_tokens,
+                        int32_t q_heads, int32_t head_dim, int32_t dtype, hipStream_t stream);
+}  // namespace sa

@@ -1,0 +1,495 @@
+// Transfer pipeline of the streamed exact-attention path: caller-pinned host
+// Q/K/V -> HBM workspace (resident Q super-block + K/V ring) -> update and
+// finalize kernels -> pinned host output.
+//
+// The fence graph follows TritonExecutorMixin._run_triton (reference
+// src/seqattn_core/streaming/executor.py:18-188) and CudaWorkspace
+// (src/seqattn_core/streaming/workspace.py:8-50):
+//   H2D stream : [wait q_free] Q copy, record q_ready;
+//                per K/V chunk [wait kv_free[slot]] K,V copies, record kv_ready[slot]
+//   compute    : wait q_ready; per chunk wait kv_ready[slot], update launch,
+//                record kv_free[slot]; record q_free (unless output reuses Q);
+//                [wait out_free[slot]] finalize; record out_ready[slot]
+//   D2H stream : wait out_ready[slot], output copy, record out_free[slot]
+//                (and q_free when the output lives in the Q buffer)
+// Copies are hipMemcpyAsync on two dedicated default-priority streams, so
+// PCIe traffic in both directions overlaps the kernels on the compute stream.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <new>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "sa_common.h"
+
+namespace sa {
+
+namespace {
+thread_local std::string g_last_error;
+}
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+}
+
+void clear_error() { g_last_error.clear(); }
+
+int32_t hip_status(hipError_t err, const char* what) {
+  if (err == hipSuccess) return 0;
+  set_error("%s failed: %s (%d)", what, hipGetErrorString(err), (int)err);
+  return (int32_t)err > 0 ? (int32_t)err : 1;
+}
+
+}  // namespace sa
+
+struct sa_pipeline {
+  int device = 0;
+  void* q_buffer = nullptr;
+  void* k_slots[3] = {nullptr, nullptr, nullptr};
+  void* v_slots[3] = {nullptr, nullptr, nullptr};
+  int num_kv = 0;
+  float* m = nullptr;
+  float* l = nullptr;
+  float* acc = nullptr;
+  void* out_slots[2] = {nullptr, nullptr};
+  bool has_out_slots = false;
+  int num_out = 0;
+  int q_chunk = 0, kv_chunk = 0, q_heads = 0, kv_heads = 0, head_dim = 0, dtype = 0;
+  int64_t q_row_bytes = 0, kv_row_bytes = 0;
+
+  hipStream_t h2d = nullptr, d2h = nullptr;
+  bool owns_streams = false;
+  hipEvent_t q_ready = nullptr, q_free = nullptr;
+  hipEvent_t kv_ready[3] = {}, kv_free[3] = {};
+  hipEvent_t out_ready[2] = {}, out_free[2] = {};
+  bool q_pending = false;
+  bool kv_pending[3] = {false, false, false};
+  bool out_pending[2] = {false, false};
+};
+
+namespace {
+
+void add_stats(sa_pipeline_stats* st, int64_t h2d, int64_t d2h, int64_t qc, int64_t kvt,
+               int64_t resident) {
+  if (!st) return;
+  st->h2d_bytes += h2d;
+  st->d2h_bytes += d2h;
+  st->q_chunks += qc;
+  st->kv_tiles += kvt;
+  st->max_resident_q_tokens = std::max(st->max_resident_q_tokens, resident);
+}
+
+void release(sa_pipeline* p) {
+  if (p->h2d) hipStreamSynchronize(p->h2d);
+  if (p->d2h) hipStreamSynchronize(p->d2h);
+  hipEvent_t* evs[] = {&p->q_ready, &p->q_free};
+  for (hipEvent_t* e : evs)
+    if (*e) hipEventDestroy(*e);
+  for (int i = 0; i < 3; ++i) {
+    if (p->kv_ready[i]) hipEventDestroy(p->kv_ready[i]);
+    if (p->kv_free[i]) hipEventDestroy(p->kv_free[i]);
+  }
+  for (int i = 0; i < 2; ++i) {
+    if (p->out_ready[i]) hipEventDestroy(p->out_ready[i]);
+    if (p->out_free[i]) hipEventDestroy(p->out_free[i]);
+  }
+  if (p->owns_streams) {
+    if (p->h2d) hipStreamDestroy(p->h2d);
+    if (p->d2h) hipStreamDestroy(p->d2h);
+  }
+}
+
+int32_t load_q(sa_pipeline* p, const void* q_host, int32_t q_tokens, hipStream_t compute,
+               sa_pipeline_stats* st) {
+  if (q_tokens < 0 || q_tokens > p->q_chunk) {
+    sa::set_error("q_tokens %d outside [0, q_chunk_tokens=%d]", q_tokens, p->q_chunk);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  const int64_t bytes = (int64_t)q_tokens * p->q_row_bytes;
+  if (p->q_pending) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->q_free, 0));
+  if (bytes > 0)
+    SA_HIP_RETURN(hipMemcpyAsync(p->q_buffer, q_host, bytes, hipMemcpyHostToDevice, p->h2d));
+  SA_HIP_RETURN(hipEventRecord(p->q_ready, p->h2d));
+  SA_HIP_RETURN(hipStreamWaitEvent(compute, p->q_ready, 0));
+  add_stats(st, bytes, 0, 1, 0, q_tokens);
+  return 0;
+}
+
+int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_t k_length,
+                  int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
+                  int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
+  if (k_length < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
+    sa::set_error("bad stream_kv sizes k_length=%d q_tokens=%d", k_length, q_tokens);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  const char* kh = static_cast<const char*>(k_host);
+  const char* vh = static_cast<const char*>(v_host);
+  // Keys at or beyond `visible_end` are masked for every query of the block
+  // under the bottom-right causal rule; their chunks change nothing and are
+  // neither copied nor launched (the first chunk always runs so the state is
+  // initialized).
+  int64_t visible_end = k_length;
+  if (causal) {
+    visible_end = (int64_t)q_local_offset + q_tokens - 1 + causal_shift + 1;
+    visible_end = std::max<int64_t>(0, std::min<int64_t>(visible_end, k_length));
+  }
+  bool initialize = true;
+  int index = 0;
+  for (int32_t start = 0; start < k_length; start += p->kv_chunk, ++index) {
+    if (!initialize && start >= visible_end) break;
+    const int32_t n = std::min(p->kv_chunk, k_length - start);
+    const int slot = index % p->num_kv;
+    const int64_t bytes = (int64_t)n * p->kv_row_bytes;
+    if (p->kv_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free[slot], 0));
+    SA_HIP_RETURN(hipMemcpyAsync(p->k_slots[slot], kh + (int64_t)start * p->kv_row_bytes, bytes,
+                                 hipMemcpyHostToDevice, p->h2d));
+    SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], vh + (int64_t)start * p->kv_row_bytes, bytes,
+                                 hipMemcpyHostToDevice, p->h2d));
+    SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
+    add_stats(st, 2 * bytes, 0, 0, 1, 0);
+    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
+    const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+    const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+    int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (initialize ? SA_FLAG_INITIALIZE : 0);
+    int32_t rc = sa::launch_update(p->q_buffer, p->k_slots[slot], p->v_slots[slot], p->m, p->l,
+                                   p->acc, qt, p->head_dim, kt, p->head_dim, kt, p->head_dim,
+                                   p->q_heads, 1, qt, p->head_dim, q_tokens, n, p->q_heads,
+                                   p->kv_heads, p->head_dim, q_local_offset, start, causal_shift,
+                                   scale, flags, p->dtype, compute);
+    if (rc != 0) return rc;
+    initialize = false;
+    SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
+    p->kv_pending[slot] = true;
+  }
+  if (initialize && q_tokens > 0) {
+    // No keys at all: still define the state (m = -inf, l = 0, acc = 0).
+    const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+    int32_t rc = sa::launch_update(p->q_buffer, p->k_slots[0], p->v_slots[0], p->m, p->l, p->acc,
+                                   qt, p->head_dim, (int64_t)p->kv_heads * p->head_dim,
+                                   p->head_dim, (int64_t)p->kv_heads * p->head_dim, p->head_dim,
+                                   p->q_heads, 1, qt, p->head_dim, q_tokens, 0, p->q_heads,
+                                   p->kv_heads, p->head_dim, q_local_offset, 0, causal_shift,
+                                   scale, SA_FLAG_INITIALIZE, p->dtype, compute);
+    if (rc != 0) return rc;
+  }
+  return 0;
+}
+
+int32_t finalize(sa_pipeline* p, int32_t slot, int32_t q_tokens, float* lse, int64_t lse_sh,
+                 int64_t lse_off, hipStream_t compute) {
+  void* dest;
+  if (slot >= 0) {
+    if (!p->has_out_slots || slot >= p->num_out) {
+      sa::set_error("output slot %d unavailable (%d slots)", slot,
+                    p->has_out_slots ? p->num_out : 0);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    SA_HIP_RETURN(hipEventRecord(p->q_free, compute));
+    p->q_pending = true;
+    if (p->out_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(compute, p->out_free[slot], 0));
+    dest = p->out_slots[slot];
+  } else {
+    dest = p->q_buffer;
+  }
+  const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+  return sa::launch_finalize(p->acc, p->m, p->l, dest, lse, qt, p->head_dim, p->q_heads, 1, qt,
+                             p->head_dim, lse_sh, lse_off, q_tokens, p->q_heads, p->head_dim,
+                             p->dtype, compute);
+}
+
+int32_t d2h(sa_pipeline* p, void* dst, const void* src, int64_t bytes, int32_t slot,
+            int32_t release_q, hipStream_t compute, sa_pipeline_stats* st) {
+  if (slot < 0 || slot >= p->num_out) {
+    sa::set_error("event slot %d outside [0, %d)", slot, p->num_out);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  SA_HIP_RETURN(hipEventRecord(p->out_ready[slot], compute));
+  SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->out_ready[slot], 0));
+  if (bytes > 0) SA_HIP_RETURN(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, p->d2h));
+  SA_HIP_RETURN(hipEventRecord(p->out_free[slot], p->d2h));
+  p->out_pending[slot] = true;
+  if (release_q) {
+    SA_HIP_RETURN(hipEventRecord(p->q_free, p->d2h));
+    p->q_pending = true;
+  }
+  add_stats(st, 0, bytes, 0, 0, 0);
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int32_t sa_abi_version(void) { return SA_ABI_VERSION; }
+
+const char* sa_last_error(void) { return sa::g_last_error.c_str(); }
+
+int32_t sa_pipeline_create(sa_pipeline** out_pipeline, int32_t device, void* q_buffer,
+                           void* const* k_slots, void* const* v_slots, int32_t num_kv_buffers,
+                           float* running_max, float* running_sum, float* accumulator,
+                           void* const* out_slots, int32_t num_output_buffers,
+                           int32_t q_chunk_tokens, int32_t kv_chunk_tokens, int32_t q_heads,
+                           int32_t kv_heads, int32_t head_dim, int32_t dtype,
+                           void* h2d_stream, void* d2h_stream) {
+  sa::clear_error();
+  if (!out_pipeline) {
+    sa::set_error("sa_pipeline_create: null out_pipeline");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  *out_pipeline = nullptr;
+  if (num_kv_buffers < 1 || num_kv_buffers > 3 || num_output_buffers < 1 || num_output_buffers > 2 ||
+      q_chunk_tokens <= 0 || kv_chunk_tokens <= 0 || q_heads <= 0 || kv_heads <= 0 ||
+      q_heads % kv_heads != 0 || head_dim <= 0 || head_dim % 8 != 0) {
+    sa::set_error("sa_pipeline_create: invalid plan (kv buffers %d, output buffers %d, q_chunk %d, "
+                  "kv_chunk %d, heads %d/%d, head_dim %d)",
+                  num_kv_buffers, num_output_buffers, q_chunk_tokens, kv_chunk_tokens, q_heads,
+                  kv_heads, head_dim);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
+    sa::set_error("sa_pipeline_create: unsupported dtype code %d", dtype);
+    return SA_ERR_UNSUPPORTED_DTYPE;
+  }
+  if (!q_buffer || !k_slots || !v_slots || !running_max || !running_sum || !accumulator) {
+    sa::set_error("sa_pipeline_create: null workspace buffer");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa_pipeline* p = new (std::nothrow) sa_pipeline();
+  if (!p) {
+    sa::set_error("sa_pipeline_create: out of host memory");
+    return SA_ERR_BAD_STATE;
+  }
+  p->device = device;
+  p->q_buffer = q_buffer;
+  p->num_kv = num_kv_buffers;
+  for (int i = 0; i < num_kv_buffers; ++i) {
+    p->k_slots[i] = k_slots[i];
+    p->v_slots[i] = v_slots[i];
+    if (!k_slots[i] || !v_slots[i]) {
+      delete p;
+      sa::set_error("sa_pipeline_create: null K/V slot %d", i);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+  }
+  p->m = running_max;
+  p->l = running_sum;
+  p->acc = accumulator;
+  p->num_out = num_output_buffers;
+  p->has_out_slots = out_slots != nullptr;
+  if (p->has_out_slots) {
+    for (int i = 0; i < num_output_buffers; ++i) {
+      p->out_slots[i] = out_slots[i];
+      if (!out_slots[i]) {
+        delete p;
+        sa::set_error("sa_pipeline_create: null output slot %d", i);
+        return SA_ERR_INVALID_ARGUMENT;
+      }
+    }
+  }
+  p->q_chunk = q_chunk_tokens;
+  p->kv_chunk = kv_chunk_tokens;
+  p->q_heads = q_heads;
+  p->kv_heads = kv_heads;
+  p->head_dim = head_dim;
+  p->dtype = dtype;
+  p->q_row_bytes = (int64_t)q_heads * head_dim * 2;
+  p->kv_row_bytes = (int64_t)kv_heads * head_dim * 2;
+
+  sa::DeviceGuard guard(device);
+  hipError_t err = hipSuccess;
+  if ((h2d_stream == nullptr) != (d2h_stream == nullptr)) {
+    delete p;
+    sa::set_error("sa_pipeline_create: pass both copy streams or neither");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (h2d_stream) {
+    p->h2d = static_cast<hipStream_t>(h2d_stream);
+    p->d2h = static_cast<hipStream_t>(d2h_stream);
+  } else {
+    p->owns_streams = true;
+    err = hipStreamCreateWithFlags(&p->h2d, hipStreamNonBlocking);
+    if (err == hipSuccess) err = hipStreamCreateWithFlags(&p->d2h, hipStreamNonBlocking);
+  }
+  const unsigned flags = hipEventDisableTiming;
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&p->q_ready, flags);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&p->q_free, flags);
+  for (int i = 0; i < num_kv_buffers && err == hipSuccess; ++i) {
+    err = hipEventCreateWithFlags(&p->kv_ready[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->kv_free[i], flags);
+  }
+  for (int i = 0; i < num_output_buffers && err == hipSuccess; ++i) {
+    err = hipEventCreateWithFlags(&p->out_ready[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->out_free[i], flags);
+  }
+  if (err != hipSuccess) {
+    int32_t rc = sa::hip_status(err, "sa_pipeline_create stream/event creation");
+    release(p);
+    delete p;
+    return rc;
+  }
+  *out_pipeline = p;
+  return 0;
+}
+
+int32_t sa_pipeline_destroy(sa_pipeline* p) {
+  sa::clear_error();
+  if (!p) return 0;
+  {
+    sa::DeviceGuard guard(p->device);
+    release(p);
+  }
+  delete p;
+  return 0;
+}
+
+int32_t sa_pipeline_load_q(sa_pipeline* p, const void* q_host, int32_t q_tokens,
+                           void* compute_stream, sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  sa::DeviceGuard guard(p->device);
+  return load_q(p, q_host, q_tokens, static_cast<hipStream_t>(compute_stream), stats);
+}
+
+int32_t sa_pipeline_stream_kv(sa_pipeline* p, const void* k_host, const void* v_host,
+                              int32_t k_length, int32_t q_tokens, int32_t q_local_offset,
+                              int32_t causal_shift, double softmax_scale, int32_t causal,
+                              void* compute_stream, sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  sa::DeviceGuard guard(p->device);
+  return stream_kv(p, k_host, v_host, k_length, q_tokens, q_local_offset, causal_shift,
+                   softmax_scale, causal, static_cast<hipStream_t>(compute_stream), stats);
+}
+
+int32_t sa_pipeline_finalize(sa_pipeline* p, int32_t slot, int32_t q_tokens, float* lse,
+                             int64_t lse_stride_h, int64_t lse_token_offset, void* compute_stream) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  sa::DeviceGuard guard(p->device);
+  return finalize(p, slot, q_tokens, lse, lse_stride_h, lse_token_offset,
+                  static_cast<hipStream_t>(compute_stream));
+}
+
+int32_t sa_pipeline_finalize_into(sa_pipeline* p, void* dest, int64_t stride_ot,
+                                  int64_t stride_oh, int32_t q_tokens, float* lse,
+                                  int64_t lse_stride_h, int64_t lse_token_offset,
+                                  void* compute_stream) {
+  sa::clear_error();
+  if (!p || !dest) return SA_ERR_INVALID_ARGUMENT;
+  if (q_tokens < 0 || q_tokens > p->q_chunk) {
+    sa::set_error("q_tokens %d outside [0, q_chunk_tokens=%d]", q_tokens, p->q_chunk);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa::DeviceGuard guard(p->device);
+  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  SA_HIP_RETURN(hipEventRecord(p->q_free, compute));
+  p->q_pending = true;
+  const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+  return sa::launch_finalize(p->acc, p->m, p->l, dest, lse, qt, p->head_dim, p->q_heads, 1,
+                             stride_ot, stride_oh, lse_stride_h, lse_token_offset, q_tokens,
+                             p->q_heads, p->head_dim, p->dtype, compute);
+}
+
+int32_t sa_pipeline_release_q(sa_pipeline* p, void* compute_stream) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(hipEventRecord(p->q_free, static_cast<hipStream_t>(compute_stream)));
+  p->q_pending = true;
+  return 0;
+}
+
+int32_t sa_pipeline_d2h(sa_pipeline* p, void* dst_host, const void* src, int64_t bytes,
+                        int32_t event_slot, int32_t release_q, void* compute_stream,
+                        sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  sa::DeviceGuard guard(p->device);
+  return d2h(p, dst_host, src, bytes, event_slot, release_q,
+             static_cast<hipStream_t>(compute_stream), stats);
+}
+
+int32_t sa_pipeline_synchronize(sa_pipeline* p) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
+  return 0;
+}
+
+void* sa_pipeline_stream(sa_pipeline* p, int32_t which) {
+  if (!p) return nullptr;
+  return which == 0 ? static_cast<void*>(p->h2d) : static_cast<void*>(p->d2h);
+}
+
+void* sa_pipeline_output_slot(sa_pipeline* p, int32_t index) {
+  if (!p || !p->has_out_slots || index < 0 || index >= p->num_out) return nullptr;
+  return p->out_slots[index];
+}
+
+void* sa_pipeline_q_buffer(sa_pipeline* p) { return p ? p->q_buffer : nullptr; }
+
+int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, const void* v_host,
+                        void* out_host, float* lse, int64_t lse_stride_h,
+                        const int64_t* cu_seqlens_q, const int64_t* cu_seqlens_k,
+                        int32_t num_segments, double softmax_scale, int32_t causal,
+                        void* compute_stream, sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p || !q_host || !k_host || !v_host || !out_host || !cu_seqlens_q || !cu_seqlens_k ||
+      num_segments < 0) {
+    sa::set_error("sa_pipeline_run: null argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa::DeviceGuard guard(p->device);
+  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  const char* qh = static_cast<const char*>(q_host);
+  const char* kh = static_cast<const char*>(k_host);
+  const char* vh = static_cast<const char*>(v_host);
+  char* oh = static_cast<char*>(out_host);
+  int64_t chunk_index = 0;
+  for (int32_t s = 0; s < num_segments; ++s) {
+    const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
+    const int64_t k_start = cu_seqlens_k[s], k_stop = cu_seqlens_k[s + 1];
+    const int64_t q_length = q_stop - q_start, k_length = k_stop - k_start;
+    if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0)) {
+      sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    const int32_t causal_shift = (int32_t)(k_length - q_length);
+    for (int64_t qt = q_start; qt < q_stop; qt += p->q_chunk) {
+      const int32_t n = (int32_t)std::min<int64_t>(p->q_chunk, q_stop - qt);
+      int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
+      if (rc) return rc;
+      rc = stream_kv(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
+                     (int32_t)k_length, n, (int32_t)(qt - q_start), causal_shift, softmax_scale,
+                     causal, compute, stats);
+      if (rc) return rc;
+      const int32_t slot = (int32_t)(chunk_index % p->num_out);
+      const int64_t bytes = (int64_t)n * p->q_row_bytes;
+      if (p->has_out_slots) {
+        rc = finalize(p, slot, n, lse, lse_stride_h, qt, compute);
+        if (rc) return rc;
+        rc = d2h(p, oh + qt * p->q_row_bytes, p->out_slots[slot], bytes, slot, 0, compute, stats);
+      } else {
+        rc = finalize(p, -1, n, lse, lse_stride_h, qt, compute);
+        if (rc) return rc;
+        rc = d2h(p, oh + qt * p->q_row_bytes, p->q_buffer, bytes, slot, 1, compute, stats);
+      }
+      if (rc) return rc;
+      ++chunk_index;
+    }
+  }
+  SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
+  return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,28 @@
+"""seqattn for AMD MI355X: streamed exact attention over host-resident Q/K/V.
+
+Drop-in for the reference package's tensor-mode and device-consumer API
+(reference src/seqattn_core/__init__.py:1-77).  Q/K/V stay in caller-owned
+(pinned) host DRAM; a resident Q super-block and a K/V ring live in a bounded
+HBM workspace; the chunk-update / finalize kernels and the copy pipeline are
+native gfx950 code in ``_lib/libseqattn_hip.so``.
+"""
+
+from .api import StreamingAttentionRunner, streaming_attn_func, streaming_attn_varlen_func
+from .config import PagedAttentionConfig, StreamingAttentionConfig
+from .planner import AttentionPlan, build_plan
+from .stats import PagedAttentionStats, ProjectedAttentionStats, StreamingAttentionStats
+
+__all__ = [
+    "AttentionPlan",
+    "PagedAttentionConfig",
+    "PagedAttentionStats",
+    "ProjectedAttentionStats",
+    "StreamingAttentionConfig",
+    "StreamingAttentionRunner",
+    "StreamingAttentionStats",
+    "build_plan",
+    "streaming_attn_func",
+    "streaming_attn_varlen_func",
+]
+
+__version__ = "0.3.0+mi355x"

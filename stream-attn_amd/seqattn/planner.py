@@ -1,0 +1,296 @@
+"""Workspace planner: sizes the resident Q super-block and the K/V chunk.
+
+Restates the reference planner (src/seqattn_core/planner.py:11-325) so that a
+plan built here for the same shape and budget has the same q_chunk_tokens,
+kv_chunk_tokens and estimated bytes (pinned against the reference README's
+524,288-token workspace sweep and its planner tests).
+
+* ``estimate_workspace_bytes`` (reference L78-104): resident Q + FP32 state
+  (acc + m + l = head_dim + 2 floats per query head) + raw output slots (host
+  mode only) + the K/V ring + a fixed 32 MiB margin.
+* ``_largest_q_chunk_that_fits`` (L107-155): binary search over block_m
+  multiples.
+* ``_candidate_cost`` (L158-184): PCIe / state-traffic / launch cost model
+  used to pick the K/V chunk jointly with Q.
+
+gfx950 specifics: on a ROCm device the launch preset is the native kernel's
+real tile (128 queries x 64 keys, 4 wavefronts, 2 stages) for every head_dim,
+and ``output_mode="host_aliased"`` charges no raw output slots because the
+output is finalized into the Q buffer.
+"""
+
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, replace
+
+import torch
+
+from .config import StreamingAttentionConfig
+
+FIXED_MARGIN_BYTES = 32 * 2**20
+KV_CHUNK_CANDIDATES = (4096, 8192, 16384)
+
+_PORTABLE_KERNEL = (64, 64, 4, 2)
+_GFX950_KERNEL = (128, 64, 4, 2)
+
+
+def _align_down(value: int, alignment: int) -> int:
+    return value - value % alignment
+
+
+def _element_size(dtype: torch.dtype) -> int:
+    return torch.empty((), dtype=dtype).element_size()
+
+
+def _charges_output_slots(output_mode: str) -> bool:
+    return output_mode == "host"
+
+
+def _is_rocm_gpu(device: torch.device) -> bool:
+    return device.type == "cuda" and torch.version.hip is not None and torch.cuda.is_available()
+
+
+def _resolve_kernel_config(
+    config: StreamingAttentionConfig,
+    *,
+    device: torch.device,
+    head_dim: int,
+    dtype: torch.dtype,
+) -> StreamingAttentionConfig:
+    """Fill unset launch parameters (reference planner.py:19-49).
+
+    Any explicit launch parameter selects the portable baseline for the rest;
+    with none set, a ROCm device with float16/bfloat16 inputs gets the gfx950
+    preset and everything else the portable one.
+    """
+    values = (config.block_m, config.block_n, config.num_warps, config.num_stages)
+    base = _PORTABLE_KERNEL
+    if all(value is None for value in values):
+        if _is_rocm_gpu(device) and dtype in {torch.float16, torch.bfloat16}:
+            base = _GFX950_KERNEL
+    block_m, block_n, num_warps, num_stages = (
+        default if value is None else value for value, default in zip(values, base)
+    )
+    return replace(
+        config, block_m=block_m, block_n=block_n, num_warps=num_warps, num_stages=num_stages
+    )
+
+
+@dataclass(frozen=True)
+class AttentionPlan:
+    q_heads: int
+    kv_heads: int
+    head_dim: int
+    dtype: torch.dtype
+    device: torch.device
+    max_q_tokens: int
+    max_kv_tokens: int
+    q_chunk_tokens: int
+    kv_chunk_tokens: int
+    num_kv_buffers: int
+    num_output_buffers: int
+    output_mode: str
+    block_m: int
+    block_n: int
+    num_warps: int
+    num_stages: int
+    estimated_workspace_bytes: int
+    workspace_budget_bytes: int | None
+
+    @property
+    def group_size(self) -> int:
+        return self.q_heads // self.kv_heads
+
+    @property
+    def q_passes(self) -> int:
+        """Passes over K/V for one segment of max_q_tokens queries."""
+        return math.ceil(self.max_q_tokens / self.q_chunk_tokens)
+
+
+def estimate_workspace_bytes(
+    *,
+    q_tokens: int,
+    kv_tokens: int,
+    q_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+    num_kv_buffers: int,
+    num_output_buffers: int,
+    output_mode: str = "host",
+) -> int:
+    element = _element_size(dtype)
+    resident_q = q_tokens * q_heads * head_dim * element
+    state = q_tokens * q_heads * (head_dim + 2) * 4  # fp32 acc, m, l
+    outputs = (
+        num_output_buffers * q_tokens * q_heads * head_dim * element
+        if _charges_output_slots(output_mode)
+        else 0
+    )
+    ring = num_kv_buffers * 2 * kv_tokens * kv_heads * head_dim * element
+    return resident_q + state + outputs + ring + FIXED_MARGIN_BYTES
+
+
+def _workspace_for(q_tokens: int, kv_tokens: int, shape: dict, config: StreamingAttentionConfig) -> int:
+    return estimate_workspace_bytes(
+        q_tokens=q_tokens,
+        kv_tokens=kv_tokens,
+        num_kv_buffers=config.num_kv_buffers,
+        num_output_buffers=config.num_output_buffers,
+        output_mode=config.output_mode,
+        **shape,
+    )
+
+
+def _largest_q_chunk_that_fits(
+    *,
+    max_q_tokens: int,
+    kv_tokens: int,
+    q_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+    config: StreamingAttentionConfig,
+) -> int | None:
+    """Largest block_m-aligned resident Q (at least one block) within the budget."""
+    shape = {"q_heads": q_heads, "kv_heads": kv_heads, "head_dim": head_dim, "dtype": dtype}
+    step = config.block_m
+    floor_q = min(step, max_q_tokens)
+    budget = config.workspace_budget_bytes
+    if budget is None:
+        return max_q_tokens
+    if _workspace_for(floor_q, kv_tokens, shape, config) > budget:
+        return None
+    lo, hi, best = floor_q, max_q_tokens, floor_q
+    while lo <= hi:
+        probe = max(_align_down((lo + hi) // 2, step), floor_q)
+        if _workspace_for(probe, kv_tokens, shape, config) <= budget:
+            best = probe
+            lo = probe + step
+        else:
+            hi = probe - step
+    return min(best, max_q_tokens)
+
+
+def _candidate_cost(
+    *,
+    q_chunk: int,
+    kv_chunk: int,
+    max_q_tokens: int,
+    max_kv_tokens: int,
+    q_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+) -> float:
+    """Seconds estimate: K/V re-streaming over PCIe, FP32 state traffic, launches."""
+    element = _element_size(dtype)
+    passes = math.ceil(max_q_tokens / q_chunk)
+    chunks = math.ceil(max_kv_tokens / kv_chunk)
+    kv_stream_bytes = passes * 2 * max_kv_tokens * kv_heads * head_dim * element
+    state_bytes = chunks * 2 * max_q_tokens * q_heads * (head_dim + 2) * 4
+    launches = passes * (chunks + 1)
+    # Chunks smaller than 8K pay launch/overlap overhead, larger ones lose
+    # ring overlap; both are penalized relative to 8K.
+    octaves = math.log2(kv_chunk / 8192)
+    overlap = 1.0 + 0.08 * max(-octaves, 0.0) + 0.65 * max(octaves, 0.0)
+    return kv_stream_bytes * overlap / 24e9 + state_bytes / 1.2e12 + launches * 8e-6
+
+
+def build_plan(
+    *,
+    q_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+    device: torch.device | str,
+    max_q_tokens: int,
+    max_kv_tokens: int,
+    config: StreamingAttentionConfig | None = None,
+) -> AttentionPlan:
+    """Choose (q_chunk_tokens, kv_chunk_tokens) for a shape and budget."""
+    config = StreamingAttentionConfig() if config is None else config
+    config.validate()
+    device = torch.device(device)
+    if device.type == "cuda" and device.index is None and torch.cuda.is_available():
+        device = torch.device("cuda", torch.cuda.current_device())
+    if q_heads <= 0 or kv_heads <= 0 or q_heads % kv_heads:
+        raise ValueError("q_heads must be a positive multiple of kv_heads")
+    if head_dim <= 0 or head_dim > 256 or head_dim % 8:
+        raise ValueError("head_dim must be a multiple of 8 and at most 256")
+    if dtype not in {torch.float16, torch.bfloat16, torch.float32}:
+        raise ValueError("dtype must be float16, bfloat16, or float32")
+    if max_q_tokens <= 0 or max_kv_tokens <= 0:
+        raise ValueError("max_q_tokens and max_kv_tokens must be positive")
+    config = _resolve_kernel_config(config, device=device, head_dim=head_dim, dtype=dtype)
+    shape = {"q_heads": q_heads, "kv_heads": kv_heads, "head_dim": head_dim, "dtype": dtype}
+
+    if config.kv_chunk_tokens is None:
+        kv_options = sorted(
+            {max(config.block_n, min(max_kv_tokens, c)) for c in KV_CHUNK_CANDIDATES}
+        )
+    else:
+        kv_options = [min(config.kv_chunk_tokens, max_kv_tokens)]
+
+    scored: list[tuple[float, int, int]] = []
+    for kv_option in kv_options:
+        kv_chunk = min(max(config.block_n, _align_down(kv_option, config.block_n)), max_kv_tokens)
+        if config.q_chunk_tokens is None:
+            q_chunk = _largest_q_chunk_that_fits(
+                max_q_tokens=max_q_tokens, kv_tokens=kv_chunk, config=config, **shape
+            )
+            if q_chunk is None:
+                continue
+        else:
+            q_chunk = max(
+                min(config.block_m, max_q_tokens),
+                _align_down(min(config.q_chunk_tokens, max_q_tokens), config.block_m),
+            )
+        cost = _candidate_cost(
+            q_chunk=q_chunk,
+            kv_chunk=kv_chunk,
+            max_q_tokens=max_q_tokens,
+            max_kv_tokens=max_kv_tokens,
+            **shape,
+        )
+        scored.append((cost, q_chunk, kv_chunk))
+
+    if not scored:
+        smallest = _workspace_for(min(config.block_m, max_q_tokens), min(kv_options), shape, config)
+        raise ValueError(
+            "workspace budget is too small for one query block and the requested KV buffers: "
+            f"need at least {smallest / 2**20:.1f} MiB"
+        )
+    _, q_chunk, kv_chunk = min(scored)
+
+    estimated = _workspace_for(q_chunk, kv_chunk, shape, config)
+    budget = config.workspace_budget_bytes
+    if budget is not None and estimated > budget:
+        raise ValueError(
+            f"requested chunks need {estimated / 2**20:.1f} MiB, exceeding the "
+            f"{budget / 2**20:.1f} MiB workspace budget"
+        )
+    return AttentionPlan(
+        q_heads=q_heads,
+        kv_heads=kv_heads,
+        head_dim=head_dim,
+        dtype=dtype,
+        device=device,
+        max_q_tokens=max_q_tokens,
+        max_kv_tokens=max_kv_tokens,
+        q_chunk_tokens=q_chunk,
+        kv_chunk_tokens=kv_chunk,
+        num_kv_buffers=config.num_kv_buffers,
+        num_output_buffers=config.num_output_buffers,
+        output_mode=config.output_mode,
+        block_m=config.block_m,
+        block_n=config.block_n,
+        num_warps=config.num_warps,
+        num_stages=config.num_stages,
+        estimated_workspace_bytes=estimated,
+        workspace_budget_bytes=budget,
+    )
+
+
+__all__ = ["AttentionPlan", "build_plan", "estimate_workspace_bytes"]

@@ -1,0 +1,82 @@
+"""Device workspace and transfer pipeline handle.
+
+Buffers follow CudaWorkspace (reference src/seqattn_core/streaming/workspace.py:8-50):
+resident Q ``[q_chunk, Hq, D]``, a K/V ring of ``num_kv_buffers`` slots
+``[kv_chunk, Hkv, D]``, FP32 state (running max/sum ``[q_chunk, Hq]``,
+accumulator ``[q_chunk, Hq, D]``) and, in host output mode, raw output slots.
+They are torch allocations, so the planner's budget accounts for all of them.
+The ready/free events live in the native pipeline object bound to these
+buffers; copies run on two torch streams handed to it and compute on torch's
+current stream at creation.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from .. import _native
+from ..planner import AttentionPlan
+
+
+class CudaWorkspace:
+    def __init__(self, plan: AttentionPlan) -> None:
+        device = plan.device
+        self.device = device
+        self.q = torch.empty((plan.q_chunk_tokens, plan.q_heads, plan.head_dim), dtype=plan.dtype, device=device)
+        self.k = [
+            torch.empty((plan.kv_chunk_tokens, plan.kv_heads, plan.head_dim), dtype=plan.dtype, device=device)
+            for _ in range(plan.num_kv_buffers)
+        ]
+        self.v = [torch.empty_like(t) for t in self.k]
+        self.running_max = torch.empty((plan.q_chunk_tokens, plan.q_heads), dtype=torch.float32, device=device)
+        self.running_sum = torch.empty_like(self.running_max)
+        self.accumulator = torch.empty(
+            (plan.q_chunk_tokens, plan.q_heads, plan.head_dim), dtype=torch.float32, device=device
+        )
+        self.output = (
+            [torch.empty_like(self.q) for _ in range(plan.num_output_buffers)]
+            if plan.output_mode == "host"
+            else []
+        )
+        self.compute_stream = torch.cuda.current_stream(device)
+        # Copy streams are torch streams (default priority) so torch's caching
+        # allocator can track their uses of workspace and consumer buffers
+        # (record_stream) for as long as those buffers live.
+        self.h2d_stream = torch.cuda.Stream(device=device)
+        self.d2h_stream = torch.cuda.Stream(device=device)
+
+        lib = _native.lib()
+        k_ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in self.k])
+        v_ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in self.v])
+        out_ptrs = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in self.output]) if self.output else None
+        handle = ctypes.c_void_p()
+        status = lib.sa_pipeline_create(
+            ctypes.byref(handle),
+            device.index if device.index is not None else torch.cuda.current_device(),
+            self.q.data_ptr(), k_ptrs, v_ptrs, plan.num_kv_buffers,
+            self.running_max.data_ptr(), self.running_sum.data_ptr(), self.accumulator.data_ptr(),
+            out_ptrs, plan.num_output_buffers,
+            plan.q_chunk_tokens, plan.kv_chunk_tokens, plan.q_heads, plan.kv_heads, plan.head_dim,
+            _native.dtype_code(plan.dtype),
+            self.h2d_stream.cuda_stream, self.d2h_stream.cuda_stream,
+        )
+        _native.check(status, "sa_pipeline_create")
+        self._lib = lib
+        self.handle = handle
+
+    def close(self) -> None:
+        handle = getattr(self, "handle", None)
+        if handle is not None and handle.value:
+            self._lib.sa_pipeline_destroy(handle)
+            self.handle = None
+
+    def __del__(self) -> None:
+        try:
+            self.close()
+        except Exception:  # noqa: BLE001 - interpreter shutdown
+            pass
+
+
+__all__ = ["CudaWorkspace"]

@@ -1,0 +1,70 @@
+"""The C-ABI library loads in-process and exports every symbol the header declares."""
+
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from seqattn import _native
+from seqattn.streaming import resolve_backend
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "seqattn_hip.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    return sorted(set(re.findall(r"^\s*(?:int32_t|void\*|const char\*)\s+(sa_\w+)\s*\(", text, re.M)))
+
+
+def test_header_and_binding_agree():
+    declared = declared_functions()
+    assert declared, "no declarations parsed"
+    assert set(declared) == set(_native.SIGNATURES)
+
+
+@pytest.mark.skipif(not _native.library_is_built(), reason="native library not built")
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.sa_abi_version() == _native.ABI_VERSION
+    assert lib.sa_last_error() == b""
+
+
+@pytest.mark.skipif(not _native.library_is_built(), reason="native library not built")
+def test_library_shares_torchs_hip_runtime():
+    _native.lib()
+    maps = Path("/proc/self/maps").read_text()
+    runtimes = {line.split()[-1] for line in maps.splitlines() if "libamdhip64" in line}
+    assert len(runtimes) == 1, runtimes
+    assert any("libseqattn_hip.so" in line for line in maps.splitlines())
+
+
+@pytest.mark.skipif(not _native.library_is_built(), reason="native library not built")
+def test_argument_errors_surface_without_a_gpu():
+    lib = _native.lib()
+    status = lib.sa_update_attention_state(
+        None, None, None, None, None, None, *([0] * 10), 4, 4, 4, 4, 12, 0, 0, 0, 1.0, 0, 0, None)
+    assert status == -3  # SA_ERR_UNSUPPORTED_HEAD_DIM (12 is not a multiple of 8)
+    assert b"head_dim" in lib.sa_last_error()
+    status = lib.sa_update_attention_state(
+        None, None, None, None, None, None, *([0] * 10), 4, 4, 4, 4, 64, 0, 0, 0, 1.0, 0, 7, None)
+    assert status == -2
+    with pytest.raises(RuntimeError, match="head_dim"):
+        _native.check(lib.sa_finalize_attention(
+            None, None, None, None, None, *([0] * 8), 4, 4, 12, 0, None), "finalize")
+
+
+def test_backend_resolution_never_falls_back_to_cpu():
+    with pytest.raises(ValueError, match="not part of this package"):
+        resolve_backend("reference", torch.bfloat16, torch.device("cpu"))
+    with pytest.raises(ValueError, match="ROCm"):
+        resolve_backend("auto", torch.bfloat16, torch.device("cpu"))
+    with pytest.raises(ValueError, match="float16 or bfloat16"):
+        resolve_backend("auto", torch.float32, torch.device("cuda"))
+    with pytest.raises(ValueError, match="head_dim >= 16"):
+        resolve_backend("triton", torch.bfloat16, torch.device("cuda"), head_dim=8)
+    if not torch.cuda.is_available():
+        with pytest.raises(RuntimeError, match="not available"):
+            resolve_backend("hip", torch.bfloat16, torch.device("cuda"), head_dim=64)

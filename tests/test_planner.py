@@ -1,0 +1,141 @@
+"""Planner parity: reference known answers (tests/test_planner.py of the
+reference) and the published resident-Q rows (README.md:61-68, perf doc)."""
+
+import json
+import math
+from pathlib import Path
+
+import pytest
+import torch
+
+from seqattn import StreamingAttentionConfig, build_plan
+from seqattn.planner import estimate_workspace_bytes
+
+GOLDEN = json.loads((Path(__file__).parent / "golden" / "planner_reference_rows.json").read_text())
+
+
+def test_planner_uses_largest_query_chunk_that_fits_budget():
+    shape = {"q_heads": 16, "kv_heads": 4, "head_dim": 64, "dtype": torch.bfloat16,
+             "num_kv_buffers": 2, "num_output_buffers": 2}
+    budget = estimate_workspace_bytes(q_tokens=512, kv_tokens=256, **shape)
+    plan = build_plan(
+        q_heads=16, kv_heads=4, head_dim=64, dtype=torch.bfloat16, device="cpu",
+        max_q_tokens=2048, max_kv_tokens=2048,
+        config=StreamingAttentionConfig(workspace_budget_bytes=budget, kv_chunk_tokens=256,
+                                        num_output_buffers=2),
+    )
+    assert plan.q_chunk_tokens == 512
+    assert plan.estimated_workspace_bytes <= budget
+    assert plan.group_size == 4
+
+
+def test_planner_rejects_invalid_gqa_ratio():
+    with pytest.raises(ValueError, match="multiple"):
+        build_plan(q_heads=6, kv_heads=4, head_dim=64, dtype=torch.bfloat16, device="cpu",
+                   max_q_tokens=16, max_kv_tokens=16)
+
+
+def test_planner_rejects_explicit_chunks_over_budget():
+    with pytest.raises(ValueError, match="exceeding"):
+        build_plan(q_heads=16, kv_heads=4, head_dim=64, dtype=torch.bfloat16, device="cpu",
+                   max_q_tokens=2048, max_kv_tokens=2048,
+                   config=StreamingAttentionConfig(workspace_budget_bytes=40 * 2**20,
+                                                   q_chunk_tokens=2048, kv_chunk_tokens=1024))
+
+
+def test_planner_rejects_budget_below_one_block():
+    with pytest.raises(ValueError, match="too small"):
+        build_plan(q_heads=56, kv_heads=56, head_dim=128, dtype=torch.bfloat16, device="cpu",
+                   max_q_tokens=65536, max_kv_tokens=65536,
+                   config=StreamingAttentionConfig(workspace_budget_bytes=40 * 2**20))
+
+
+def test_joint_planner_prefers_8k_kv_and_large_resident_q_for_h3_shape():
+    plan = build_plan(q_heads=56, kv_heads=8, head_dim=128, dtype=torch.bfloat16, device="cpu",
+                      max_q_tokens=61_312, max_kv_tokens=61_312,
+                      config=StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30,
+                                                      output_mode="device_consumer"))
+    assert plan.kv_chunk_tokens == 8192
+    assert 43_000 <= plan.q_chunk_tokens <= 50_000
+    assert plan.estimated_workspace_bytes <= 2 * 2**30
+
+
+def test_device_consumer_plan_does_not_charge_raw_output_buffer():
+    shape = {"q_tokens": 512, "kv_tokens": 256, "q_heads": 16, "kv_heads": 4, "head_dim": 64,
+             "dtype": torch.bfloat16, "num_kv_buffers": 2, "num_output_buffers": 2}
+    host = estimate_workspace_bytes(**shape, output_mode="host")
+    consumer = estimate_workspace_bytes(**shape, output_mode="device_consumer")
+    aliased = estimate_workspace_bytes(**shape, output_mode="host_aliased")
+    assert host - consumer == 2 * 512 * 16 * 64 * 2
+    assert aliased == consumer
+
+
+def test_default_kernel_profile_is_portable_on_cpu():
+    plan = build_plan(q_heads=8, kv_heads=8, head_dim=128, dtype=torch.bfloat16, device="cpu",
+                      max_q_tokens=1024, max_kv_tokens=1024)
+    assert (plan.block_m, plan.block_n, plan.num_warps, plan.num_stages) == (64, 64, 4, 2)
+
+
+def test_explicit_kernel_parameter_uses_portable_defaults_for_the_rest():
+    plan = build_plan(q_heads=8, kv_heads=8, head_dim=128, dtype=torch.bfloat16, device="cpu",
+                      max_q_tokens=1024, max_kv_tokens=1024,
+                      config=StreamingAttentionConfig(block_m=32))
+    assert (plan.block_m, plan.block_n, plan.num_warps, plan.num_stages) == (32, 64, 4, 2)
+
+
+@pytest.mark.parametrize("row", GOLDEN["sweep_524k"]["rows"], ids=lambda r: f"{r['workspace_gib']}GiB")
+def test_planner_reproduces_published_524k_sweep(row):
+    g = GOLDEN["sweep_524k"]
+    plan = build_plan(
+        q_heads=g["q_heads"], kv_heads=g["kv_heads"], head_dim=g["head_dim"], dtype=torch.bfloat16,
+        device="cpu", max_q_tokens=g["tokens"], max_kv_tokens=g["tokens"],
+        config=StreamingAttentionConfig(workspace_budget_bytes=row["workspace_gib"] * 2**30,
+                                        block_m=g["block_m"], kv_chunk_tokens=g["kv_chunk_tokens"]),
+    )
+    assert plan.q_chunk_tokens == row["resident_q"]
+    assert plan.q_passes == row["q_passes"]
+    qkv_bytes = g["tokens"] * g["q_heads"] * g["head_dim"] * 2
+    h2d_gib = (qkv_bytes + plan.q_passes * 2 * qkv_bytes) / 2**30
+    assert round(h2d_gib) == row["h2d_gib"]
+
+
+@pytest.mark.parametrize("row", GOLDEN["kv_chunk_61k"]["rows"], ids=lambda r: str(r["kv_chunk_tokens"]))
+def test_planner_reproduces_published_61k_kv_chunk_rows(row):
+    g = GOLDEN["kv_chunk_61k"]
+    plan = build_plan(
+        q_heads=g["q_heads"], kv_heads=g["kv_heads"], head_dim=g["head_dim"], dtype=torch.bfloat16,
+        device="cpu", max_q_tokens=g["tokens"], max_kv_tokens=g["tokens"],
+        config=StreamingAttentionConfig(workspace_budget_bytes=g["workspace_gib"] * 2**30,
+                                        block_m=g["block_m"], kv_chunk_tokens=row["kv_chunk_tokens"]),
+    )
+    assert plan.q_chunk_tokens == row["resident_q"]
+
+
+def test_host_aliased_output_grows_resident_q():
+    common = dict(q_heads=56, kv_heads=56, head_dim=128, dtype=torch.bfloat16, device="cpu",
+                  max_q_tokens=524288, max_kv_tokens=524288)
+    host = build_plan(**common, config=StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30, block_m=128))
+    aliased = build_plan(**common, config=StreamingAttentionConfig(
+        workspace_budget_bytes=2 * 2**30, block_m=128, output_mode="host_aliased"))
+    assert aliased.q_chunk_tokens > host.q_chunk_tokens
+    assert aliased.q_passes < host.q_passes
+    assert aliased.estimated_workspace_bytes <= 2 * 2**30
+
+
+def test_planned_workspace_is_monotone_in_budget():
+    previous = 0
+    for gib in (1, 2, 4, 8, 14):
+        plan = build_plan(q_heads=56, kv_heads=56, head_dim=128, dtype=torch.bfloat16, device="cpu",
+                          max_q_tokens=524288, max_kv_tokens=524288,
+                          config=StreamingAttentionConfig(workspace_budget_bytes=gib * 2**30,
+                                                          block_m=128, kv_chunk_tokens=8192))
+        assert plan.q_chunk_tokens % 128 == 0
+        assert plan.q_chunk_tokens >= previous
+        assert plan.estimated_workspace_bytes <= gib * 2**30
+        # one more block would not fit
+        bigger = estimate_workspace_bytes(
+            q_tokens=plan.q_chunk_tokens + 128, kv_tokens=8192, q_heads=56, kv_heads=56, head_dim=128,
+            dtype=torch.bfloat16, num_kv_buffers=2, num_output_buffers=1)
+        assert plan.q_chunk_tokens == 524288 or bigger > gib * 2**30
+        previous = plan.q_chunk_tokens
+    assert math.ceil(524288 / previous) == 3
