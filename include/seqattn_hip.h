@@ -235,6 +235,15 @@ int32_t sa_pipeline_d2h(sa_pipeline* pipeline, void* dst_host, const void* src, 
 /* Block until the D2H stream has drained. */
 int32_t sa_pipeline_synchronize(sa_pipeline* pipeline);
 
+/*
+ * Kernel timing of the update launches: with enable != 0, every later update
+ * launch of the pipeline is bracketed by a pair of timing events on the
+ * compute stream.  sa_pipeline_kernel_timing waits for the recorded launches,
+ * returns their summed duration (ms) and count, and resets the record.
+ */
+int32_t sa_pipeline_set_kernel_timing(sa_pipeline* pipeline, int32_t enable);
+int32_t sa_pipeline_kernel_timing(sa_pipeline* pipeline, double* total_ms, int64_t* launches);
+
 /* hipStream_t of the pipeline's H2D (which == 0) or D2H (which == 1) copy stream. */
 void* sa_pipeline_stream(sa_pipeline* pipeline, int32_t which);
 

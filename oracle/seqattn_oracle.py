@@ -38,6 +38,14 @@ def segment_bounds(cu: np.ndarray | list[int], total: int, name: str) -> list[in
     return bounds
 
 
+def as_f32(x: np.ndarray) -> np.ndarray:
+    """float32 view of an input: uint16 arrays hold bfloat16 bit patterns
+    (numpy has no bfloat16), which widen exactly by a 16-bit shift."""
+    if x.dtype == np.uint16:
+        return (x.astype(np.uint32) << 16).view(np.float32)
+    return x.astype(np.float32, copy=False)
+
+
 def _validate(q, k, v, cu_q, cu_k):
     """Shape/segment checks of reference validation.py:6-47."""
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
@@ -58,6 +66,50 @@ def _validate(q, k, v, cu_q, cu_k):
     return qb, kb
 
 
+def _attend_heads(q_tile, k, v, kv_range, group, k_start, k_stop, kv_chunk, scale, causal,
+                  q_pos, causal_shift):
+    """Online-softmax recurrence of one Q tile over one segment's K/V for the
+    K/V heads in kv_range and their query heads (reference reference.py:53-107)."""
+    a, b = kv_range
+    qt = np.ascontiguousarray(as_f32(q_tile[:, a * group : b * group]).transpose(1, 0, 2))  # [h, n, D]
+    heads, n, head_dim = qt.shape
+    m = np.full((heads, n), -np.inf, dtype=np.float32)
+    l = np.zeros((heads, n), dtype=np.float32)
+    o = np.zeros((heads, n, head_dim), dtype=np.float32)
+    for kv_start in range(k_start, k_stop, kv_chunk):
+        kv_stop = min(kv_start + kv_chunk, k_stop)
+        kt = as_f32(k[kv_start:kv_stop, a:b])
+        vt = as_f32(v[kv_start:kv_stop, a:b])
+        if group != 1:
+            kt = np.repeat(kt, group, axis=1)
+            vt = np.repeat(vt, group, axis=1)
+        kt = np.ascontiguousarray(kt.transpose(1, 0, 2))  # [h, n_k, D]
+        vt = np.ascontiguousarray(vt.transpose(1, 0, 2))
+        s = np.matmul(qt, kt.transpose(0, 2, 1))
+        s *= np.float32(scale)
+        if causal:
+            k_pos = np.arange(kv_start - k_start, kv_stop - k_start)
+            visible = k_pos[None, :] <= (q_pos[:, None] + causal_shift)
+            s = np.where(visible[None], s, -np.inf).astype(np.float32)
+        tile_max = s.max(axis=-1)
+        merged = np.maximum(m, tile_max)
+        finite = np.isfinite(merged)
+        with np.errstate(invalid="ignore"):
+            alpha = np.where(finite, np.exp(m - merged), np.float32(1.0)).astype(np.float32)
+            if causal:
+                p = np.where(np.isfinite(s), np.exp(s - merged[..., None]), np.float32(0.0))
+                p = p.astype(np.float32)
+            else:
+                # Without a mask every logit is finite: p = exp(s - m') in place.
+                p = s
+                p -= merged[..., None]
+                np.exp(p, out=p)
+        l = l * alpha + p.sum(axis=-1, dtype=np.float32)
+        o = o * alpha[..., None] + np.matmul(p, vt)
+        m = np.where(finite, merged, m)
+    return m, l, o
+
+
 def chunked_attention(
     q: np.ndarray,
     k: np.ndarray,
@@ -70,6 +122,7 @@ def chunked_attention(
     softmax_scale: float | None = None,
     causal: bool = False,
     rows: np.ndarray | None = None,
+    workers: int = 1,
 ) -> tuple[np.ndarray, np.ndarray]:
     """FP32 online-softmax attention; returns (O [T, H, D] fp32, LSE [H, T] fp32).
 
@@ -86,7 +139,9 @@ def chunked_attention(
     ``rows`` (optional, sorted global query indices) restricts the work to
     those query rows: each Q tile is intersected with them, which leaves the
     per-row recurrence unchanged.  Returned arrays are full-size; rows not
-    computed are NaN.
+    computed are NaN.  ``workers > 1`` splits the K/V heads over threads
+    (numpy releases the GIL in its kernels); each head's arithmetic is the
+    same as with one worker.
     """
     q = np.asarray(q)
     k = np.asarray(k)
@@ -113,36 +168,26 @@ def chunked_attention(
                 idx = idx[row_mask[tile_start:tile_stop]]
                 if idx.size == 0:
                     continue
-            qt = np.ascontiguousarray(q[idx].astype(np.float32).transpose(1, 0, 2))  # [H, n, D]
-            n = idx.size
-            m = np.full((heads, n), -np.inf, dtype=np.float32)
-            l = np.zeros((heads, n), dtype=np.float32)
-            o = np.zeros((heads, n, head_dim), dtype=np.float32)
             q_pos = idx - q_start
-            for kv_start in range(k_start, k_stop, kv_chunk_tokens):
-                kv_stop = min(kv_start + kv_chunk_tokens, k_stop)
-                kt = k[kv_start:kv_stop].astype(np.float32)
-                vt = v[kv_start:kv_stop].astype(np.float32)
-                if group != 1:
-                    kt = np.repeat(kt, group, axis=1)
-                    vt = np.repeat(vt, group, axis=1)
-                kt = kt.transpose(1, 0, 2)  # [H, n_k, D]
-                vt = vt.transpose(1, 0, 2)
-                s = np.matmul(qt, kt.transpose(0, 2, 1)) * np.float32(scale)
-                if causal:
-                    k_pos = np.arange(kv_start - k_start, kv_stop - k_start)
-                    visible = k_pos[None, :] <= (q_pos[:, None] + causal_shift)
-                    s = np.where(visible[None], s, -np.inf).astype(np.float32)
-                tile_max = s.max(axis=-1)
-                merged = np.maximum(m, tile_max)
-                finite = np.isfinite(merged)
-                with np.errstate(invalid="ignore"):
-                    alpha = np.where(finite, np.exp(m - merged), np.float32(1.0)).astype(np.float32)
-                    p = np.where(np.isfinite(s), np.exp(s - merged[..., None]), np.float32(0.0))
-                p = p.astype(np.float32)
-                l = l * alpha + p.sum(axis=-1, dtype=np.float32)
-                o = o * alpha[..., None] + np.matmul(p, vt)
-                m = np.where(finite, merged, m)
+            q_tile = q[idx]
+            kv_heads = k.shape[1]
+            if workers > 1 and kv_heads > 1:
+                from concurrent.futures import ThreadPoolExecutor
+
+                groups = np.array_split(np.arange(kv_heads), min(workers, kv_heads))
+                jobs = [(int(g[0]), int(g[-1]) + 1) for g in groups if g.size]
+                with ThreadPoolExecutor(max_workers=len(jobs)) as pool:
+                    parts = list(pool.map(
+                        lambda job: _attend_heads(
+                            q_tile, k, v, job, group, k_start, k_stop, kv_chunk_tokens, scale, causal,
+                            q_pos, causal_shift),
+                        jobs))
+                m = np.concatenate([p[0] for p in parts])
+                l = np.concatenate([p[1] for p in parts])
+                o = np.concatenate([p[2] for p in parts])
+            else:
+                m, l, o = _attend_heads(q_tile, k, v, (0, kv_heads), group, k_start, k_stop,
+                                        kv_chunk_tokens, scale, causal, q_pos, causal_shift)
             positive = l > 0
             with np.errstate(divide="ignore", invalid="ignore"):
                 normalized = np.where(positive[..., None], o / l[..., None], np.float32(0.0))

@@ -23,6 +23,7 @@
 #include <cstdio>
 #include <cstring>
 #include <string>
+#include <vector>
 
 #include "sa_common.h"
 
@@ -74,6 +75,11 @@ struct sa_pipeline {
   bool q_pending = false;
   bool kv_pending[3] = {false, false, false};
   bool out_pending[2] = {false, false};
+
+  // Optional timing of update launches (event pairs on the compute stream).
+  bool timing = false;
+  std::vector<hipEvent_t> t_start, t_stop;
+  size_t t_used = 0;
 };
 
 namespace {
@@ -102,6 +108,8 @@ void release(sa_pipeline* p) {
     if (p->out_ready[i]) hipEventDestroy(p->out_ready[i]);
     if (p->out_free[i]) hipEventDestroy(p->out_free[i]);
   }
+  for (hipEvent_t e : p->t_start) hipEventDestroy(e);
+  for (hipEvent_t e : p->t_stop) hipEventDestroy(e);
   if (p->owns_streams) {
     if (p->h2d) hipStreamDestroy(p->h2d);
     if (p->d2h) hipStreamDestroy(p->d2h);
@@ -160,12 +168,23 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
     const int64_t qt = (int64_t)p->q_heads * p->head_dim;
     const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
     int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (initialize ? SA_FLAG_INITIALIZE : 0);
+    if (p->timing) {
+      if (p->t_used == p->t_start.size()) {
+        hipEvent_t a = nullptr, b = nullptr;
+        SA_HIP_RETURN(hipEventCreate(&a));
+        SA_HIP_RETURN(hipEventCreate(&b));
+        p->t_start.push_back(a);
+        p->t_stop.push_back(b);
+      }
+      SA_HIP_RETURN(hipEventRecord(p->t_start[p->t_used], compute));
+    }
     int32_t rc = sa::launch_update(p->q_buffer, p->k_slots[slot], p->v_slots[slot], p->m, p->l,
                                    p->acc, qt, p->head_dim, kt, p->head_dim, kt, p->head_dim,
                                    p->q_heads, 1, qt, p->head_dim, q_tokens, n, p->q_heads,
                                    p->kv_heads, p->head_dim, q_local_offset, start, causal_shift,
                                    scale, flags, p->dtype, compute);
     if (rc != 0) return rc;
+    if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
     initialize = false;
     SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
     p->kv_pending[slot] = true;
@@ -423,6 +442,31 @@ int32_t sa_pipeline_synchronize(sa_pipeline* p) {
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
+  return 0;
+}
+
+int32_t sa_pipeline_set_kernel_timing(sa_pipeline* p, int32_t enable) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  p->timing = enable != 0;
+  p->t_used = 0;
+  return 0;
+}
+
+int32_t sa_pipeline_kernel_timing(sa_pipeline* p, double* total_ms, int64_t* launches) {
+  sa::clear_error();
+  if (!p || !total_ms || !launches) return SA_ERR_INVALID_ARGUMENT;
+  sa::DeviceGuard guard(p->device);
+  double total = 0.0;
+  for (size_t i = 0; i < p->t_used; ++i) {
+    SA_HIP_RETURN(hipEventSynchronize(p->t_stop[i]));
+    float ms = 0.f;
+    SA_HIP_RETURN(hipEventElapsedTime(&ms, p->t_start[i], p->t_stop[i]));
+    total += ms;
+  }
+  *total_ms = total;
+  *launches = (int64_t)p->t_used;
+  p->t_used = 0;
   return 0;
 }
 
