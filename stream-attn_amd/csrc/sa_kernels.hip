@@ -8,24 +8,38 @@
 // before the PV product, out = acc / l (0 where l == 0).  The finalize kernel
 // also writes LSE = (m + log2 l) * ln 2, which the reference does not produce.
 //
-// Work decomposition (update kernel):
-//   workgroup = 4 wavefronts = 128 queries of one query head; grid
-//   (ceil(q_tokens / 128), q_heads).  Wave w owns queries 32w..32w+31.
-//   K/V are streamed through LDS in 64-key tiles: K row-major
-//   [key][d], V transposed [d][key], both padded against bank conflicts.
-//   The next tile's global loads are issued before the current tile's MFMA
-//   work so HBM/L2 latency hides under compute.
+// Update kernel work decomposition:
+//   workgroup = 4 wavefronts, one per SIMD; wave w owns QB blocks of 32
+//   queries (QB = 2 for head_dim <= 128, else 1) of one query head, so a
+//   workgroup covers 128 * QB queries.  Workgroups are numbered head-major and
+//   dealt to the 8 XCDs in contiguous runs, so the workgroups resident on one
+//   XCD share one head's K/V stream in that XCD's L2.
+//   K/V stream through LDS in 64-key tiles, two stages: the tile after the one
+//   being computed is fetched by global_load_lds_dwordx4 (HBM/L2 -> LDS with
+//   no register staging) while the MFMAs run; one barrier per tile.
+//   LDS rows are row-major [key][d] with 16-byte granules XOR-swizzled by the
+//   row index, which keeps both the K operand reads (ds_read_b128, 8
+//   consecutive keys per phase) and the transposing V reads
+//   (ds_read_b64_tr_b16, 4 consecutive keys per 16-lane group) free of bank
+//   conflicts.
 //
 // MFMA mapping (v_mfma_f32_32x32x16_{bf16,f16}: A 32x16, B 16x32, C 32x32):
-//   S^T[key][query] = K . Q^T : A = K rows from LDS, B = Q fragments held in
+//   S^T[key][query] = K . Q^T : A = K rows (LDS), B = Q fragments held in
 //   registers for the whole kernel.  In the C layout a lane owns one query
-//   column and 16 key rows, so the row max / row sum of the softmax are
-//   in-lane reductions plus one exchange with lane ^ 32.
-//   O^T[d][query] += V^T . P^T : B = P^T taken straight from the S^T
-//   registers (same lane, same query), A = V^T rows from LDS.  The accumulator
-//   lane again owns one query, so the alpha rescale is a lane-uniform scalar.
-//   The contraction slot (lane half h, element e) -> key assignment only has
-//   to agree between A and B, which both sides construct identically.
+//   column and 16 key rows, so softmax row reductions are in-lane.
+//   O^T[d][query] += V^T . P^T : B = P^T straight from the S^T registers (same
+//   lane, same query), A = V^T fragments produced by ds_read_b64_tr_b16 from
+//   the row-major V tile.  The contraction slot (lane half h, element e) ->
+//   key assignment is the same on both sides: key = 16c + 8(e/4) + 4h + e%4.
+//   Each K/V fragment read from LDS feeds QB MFMAs.
+//
+// Online softmax with a thresholded rescale: the running maximum m only moves
+// (and acc, l are rescaled by exp2(m_old - m_new)) when some logit of the wave
+// exceeds m + 8; otherwise p = exp2(s*scale - m) <= 2^8 against the kept m.
+// (m, l, acc) remains an exact representation of the partial softmax:
+// out = acc / l and LSE = m + log2(l) are unchanged, and P keeps bf16's
+// relative precision.  The row sum l is accumulated per lane half and the two
+// halves are combined once when the state is written.
 
 #include <hip/hip_runtime.h>
 
@@ -41,16 +55,19 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 
+#define SA_LDS __attribute__((address_space(3)))
+#define SA_GLOBAL __attribute__((address_space(1)))
+
 constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
-constexpr int kBlockM = 32 * kWaves;  // queries per workgroup
-constexpr int kBlockN = 64;           // keys per LDS tile
-constexpr int kVtPad = 4;             // V^T row padding (elements)
-constexpr int kKPad = 8;              // K row padding (elements)
+constexpr int kTileKeys = 64;  // keys per LDS stage
+constexpr int kSubKeys = 32;   // keys per softmax step
+constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
 struct BF16 {
   __device__ static inline f32x16 mma(u32x4 a, u32x4 b, f32x16 c) {
@@ -83,78 +100,107 @@ struct UpdateParams {
   float* l;
   float* acc;
   int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, ss_t, ss_h, sa_t, sa_h;
-  int32_t q_tokens, kv_tokens, group, head_dim;
+  int32_t q_tokens, kv_tokens, group, head_dim, q_heads;
   int32_t q_local_offset, kv_local_offset, causal_shift;
+  int32_t q_blocks;       // workgroups per query head
+  int32_t xcd_run;        // ceil(q_blocks * q_heads / 8)
   float scale_log2;
 };
 
 // Row r (0..15) of a 32x32 C tile held in register i of a lane in half h.
 __device__ inline int c_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 
+template <int DP>
+struct Geometry {
+  static constexpr int G = DP / 8;             // 16-byte granules per K/V row
+  static constexpr int ROW_BYTES = DP * 2;
+  static constexpr int QB = DP <= 128 ? 2 : 1;  // 32-query blocks per wave
+  static constexpr int BLOCK_M = kWaves * 32 * QB;
+  static constexpr int TILE_BYTES = kTileKeys * ROW_BYTES;  // K (or V) part of a stage
+  static constexpr int ROWS_PER_DMA = 1024 / ROW_BYTES;     // rows per wave-wide 1 KB DMA
+  static constexpr int DMA_PER_WAVE = kTileKeys / ROWS_PER_DMA / kWaves;
+  static_assert(DMA_PER_WAVE >= 1, "tile too small for the workgroup");
+  // Granule swizzle: rows r..r+7 (r % 8 == 0) get 8 distinct XOR masks and
+  // rows r..r+3 (r % 4 == 0) masks that differ in bits 1-2.
+  __device__ static inline int swz(int row) { return (((row & 3) << 1) | ((row >> 2) & 1)) & (G - 1); }
+  __device__ static inline int offset(int row, int granule) {
+    return row * ROW_BYTES + ((granule ^ swz(row)) << 4);
+  }
+};
+
 template <typename Op, int DP, bool CAUSAL, bool INIT>
 __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) {
-  constexpr int KROW = DP + kKPad;
-  constexpr int VROW = kBlockN + kVtPad;
+  using Geo = Geometry<DP>;
+  constexpr int QB = Geo::QB;
   constexpr int QC = DP / 16;  // 16-wide d slices of the QK^T contraction
   constexpr int DB = DP / 32;  // 32-row d blocks of the PV output
-  constexpr int KL = (kBlockN * DP / 8) / kThreads;  // 16-byte K loads per thread
-  constexpr int VBLOCKS = (kBlockN / 4) * (DP / 8);  // 4-key x 8-d V blocks per tile
-  constexpr int VL = (VBLOCKS + kThreads - 1) / kThreads;
-  static_assert(KL >= 1, "tile too small for the workgroup");
+  constexpr int G = Geo::G;
 
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[kBlockN * KROW];
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[DP * VROW];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * 2 * Geo::TILE_BYTES];
+
+  // XCD-aware numbering: hardware block b runs on XCD b % 8; consecutive
+  // logical workgroups (same head, neighbouring query blocks) share an XCD.
+  const int b = blockIdx.x;
+  const int logical = (b & 7) * p.xcd_run + (b >> 3);
+  if (logical >= p.q_blocks * p.q_heads) return;
+  const int head = logical / p.q_blocks;
+  const int q_block = (logical - head * p.q_blocks) * Geo::BLOCK_M;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
   const int lr = lane & 31;
   const int hf = lane >> 5;
-
-  const int head = blockIdx.y;
   const int kv_head = head / p.group;
-  const int q_block = blockIdx.x * kBlockM;
-  const int qw0 = q_block + wave * 32;  // first query of this wave
-  const int qi = qw0 + lr;              // this lane's query
-  const bool q_ok = qi < p.q_tokens;
+  const int qw0 = q_block + wave * 32 * QB;  // first query of this wave
 
   const uint16_t* qp = p.q + (int64_t)head * p.sq_h;
   const uint16_t* kp = p.k + (int64_t)kv_head * p.sk_h;
   const uint16_t* vp = p.v + (int64_t)kv_head * p.sv_h;
 
-  // Q fragments (B operand of S^T = K Q^T): query qi, d = 16c + 8h .. +7.
-  u32x4 qf[QC];
+  // Q fragments (B operand of S^T = K Q^T): query qw0 + 32qb + lr, d = 16c + 8h .. +7.
+  u32x4 qf[QB][QC];
+  int qi[QB];
 #pragma unroll
-  for (int c = 0; c < QC; ++c) {
-    const int d = 16 * c + 8 * hf;
-    if (q_ok && d < p.head_dim)
-      qf[c] = *reinterpret_cast<const u32x4*>(qp + (int64_t)qi * p.sq_t + d);
-    else
-      qf[c] = u32x4{0, 0, 0, 0};
+  for (int qb = 0; qb < QB; ++qb) {
+    qi[qb] = qw0 + 32 * qb + lr;
+    const bool ok = qi[qb] < p.q_tokens;
+#pragma unroll
+    for (int c = 0; c < QC; ++c) {
+      const int d = 16 * c + 8 * hf;
+      if (ok && d < p.head_dim)
+        qf[qb][c] = *reinterpret_cast<const u32x4*>(qp + (int64_t)qi[qb] * p.sq_t + d);
+      else
+        qf[qb][c] = u32x4{0, 0, 0, 0};
+    }
   }
 
-  // Online-softmax state of query qi (base-2 domain).
-  float m_run = -INFINITY;
-  float l_run = 0.f;
-  f32x16 acc[DB];
+  // Online-softmax state (base-2 domain).  l_part is this lane half's share of l.
+  float m_run[QB], l_part[QB];
+  f32x16 acc[QB][DB];
 #pragma unroll
-  for (int b = 0; b < DB; ++b) acc[b] = f32x16{};
-  const int64_t srow = (int64_t)qi * p.ss_t + (int64_t)head * p.ss_h;
-  float* arow = p.acc + (int64_t)qi * p.sa_t + (int64_t)head * p.sa_h;
-  if (!INIT && q_ok) {
-    m_run = p.m[srow];
-    l_run = p.l[srow];
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_part[qb] = 0.f;
 #pragma unroll
-    for (int b = 0; b < DB; ++b) {
+    for (int d = 0; d < DB; ++d) acc[qb][d] = f32x16{};
+    if (!INIT && qi[qb] < p.q_tokens) {
+      const int64_t srow = (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+      m_run[qb] = p.m[srow];
+      l_part[qb] = hf == 0 ? p.l[srow] : 0.f;
+      const float* arow = p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const int d = 32 * b + 8 * g + 4 * hf;
-        if (d < p.head_dim) {
-          const f32x4 v4 = *reinterpret_cast<const f32x4*>(arow + d);
-          acc[b][4 * g + 0] = v4[0];
-          acc[b][4 * g + 1] = v4[1];
-          acc[b][4 * g + 2] = v4[2];
-          acc[b][4 * g + 3] = v4[3];
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = 32 * d + 8 * g + 4 * hf;
+          if (col < p.head_dim) {
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(arow + col);
+            acc[qb][d][4 * g + 0] = v4[0];
+            acc[qb][d][4 * g + 1] = v4[1];
+            acc[qb][d][4 * g + 2] = v4[2];
+            acc[qb][d][4 * g + 3] = v4[3];
+          }
         }
       }
     }
@@ -163,168 +209,179 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
   // Keys at or beyond kv_end are invisible to every query of this workgroup.
   int kv_end = p.kv_tokens;
   if (CAUSAL) {
-    const int q_last = min(p.q_tokens, q_block + kBlockM) - 1;
+    const int q_last = min(p.q_tokens, q_block + Geo::BLOCK_M) - 1;
     const int lim = p.q_local_offset + q_last + p.causal_shift - p.kv_local_offset + 1;
     kv_end = max(0, min(kv_end, lim));
   }
-  const int ntiles = (kv_end + kBlockN - 1) / kBlockN;
+  const int ntiles = (kv_end + kTileKeys - 1) / kTileKeys;
 
-  // Register staging of the next tile.
-  u32x4 kreg[KL];
-  u32x4 vreg[VL][4];
+  // Scale handling: for a positive scale the max is taken on raw logits and
+  // the scale is fused into the exponent's FMA; otherwise logits are scaled
+  // first (the max of s * c for c <= 0 is not c * max(s)).
+  const bool scale_pos = p.scale_log2 > 0.f;
+  const float cf = scale_pos ? p.scale_log2 : 1.f;
 
-  auto load_tile = [&](int kt) {
+  // HBM/L2 -> LDS DMA of key tile [kt, kt + 64) into stage st.  Rows past the
+  // chunk are clamped to its last row and granules past head_dim to granule 0:
+  // those values are finite, masked (keys) or multiplied by zero Q / never
+  // stored (d), and every address stays inside the caller's buffers.
+  auto issue_tile = [&](int kt, int st) {
+    uint8_t* k_stage = lds + st * 2 * Geo::TILE_BYTES;
+    uint8_t* v_stage = k_stage + Geo::TILE_BYTES;
 #pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int c = tid + i * kThreads;
-      const int key = c / (DP / 8);
-      const int d = (c % (DP / 8)) * 8;
-      if (kt + key < p.kv_tokens && d < p.head_dim)
-        kreg[i] = *reinterpret_cast<const u32x4*>(kp + (int64_t)(kt + key) * p.sk_t + d);
-      else
-        kreg[i] = u32x4{0, 0, 0, 0};
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int b = tid + i * kThreads;
-      const int k4 = b % (kBlockN / 4);
-      const int d = (b / (kBlockN / 4)) * 8;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kt + 4 * k4 + r;
-        if (b < VBLOCKS && key < p.kv_tokens && d < p.head_dim)
-          vreg[i][r] = *reinterpret_cast<const u32x4*>(vp + (int64_t)key * p.sv_t + d);
-        else
-          vreg[i][r] = u32x4{0, 0, 0, 0};
-      }
+    for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
+      const int chunk = wave * Geo::DMA_PER_WAVE + i;
+      const int row = chunk * Geo::ROWS_PER_DMA + lane / G;
+      const int lg = (lane % G) ^ Geo::swz(row);
+      const int grow = min(kt + row, p.kv_tokens - 1);
+      const int col = (lg * 8 < p.head_dim) ? lg * 8 : 0;
+      __builtin_amdgcn_global_load_lds(
+          (const SA_GLOBAL void*)(kp + (int64_t)grow * p.sk_t + col),
+          (SA_LDS void*)(k_stage + chunk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(
+          (const SA_GLOBAL void*)(vp + (int64_t)grow * p.sv_t + col),
+          (SA_LDS void*)(v_stage + chunk * 1024), 16, 0, 0);
     }
   };
 
-  auto store_tile = [&]() {
-#pragma unroll
-    for (int i = 0; i < KL; ++i) {
-      const int c = tid + i * kThreads;
-      const int key = c / (DP / 8);
-      const int d = (c % (DP / 8)) * 8;
-      *reinterpret_cast<u32x4*>(&k_lds[key * KROW + d]) = kreg[i];
-    }
-#pragma unroll
-    for (int i = 0; i < VL; ++i) {
-      const int b = tid + i * kThreads;
-      if (b < VBLOCKS) {
-        const int k4 = b % (kBlockN / 4);
-        const int d = (b / (kBlockN / 4)) * 8;
-        // vreg[i][r] holds V[key 4*k4 + r][d .. d+7]; emit V^T[d + e][4*k4 .. +3].
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const uint32_t x0 = vreg[i][0][w], x1 = vreg[i][1][w];
-          const uint32_t x2 = vreg[i][2][w], x3 = vreg[i][3][w];
-          const u32x2 even = {(x0 & 0xffffu) | (x1 << 16), (x2 & 0xffffu) | (x3 << 16)};
-          const u32x2 odd = {(x0 >> 16) | (x1 & 0xffff0000u), (x2 >> 16) | (x3 & 0xffff0000u)};
-          *reinterpret_cast<u32x2*>(&vt_lds[(d + 2 * w) * VROW + 4 * k4]) = even;
-          *reinterpret_cast<u32x2*>(&vt_lds[(d + 2 * w + 1) * VROW + 4 * k4]) = odd;
-        }
-      }
-    }
-  };
-
-  if (ntiles > 0) load_tile(0);
+  if (ntiles > 0) issue_tile(0, 0);
 
   for (int t = 0; t < ntiles; ++t) {
-    const int kt = t * kBlockN;
-    __syncthreads();  // every wave is done reading the previous tile
-    store_tile();
+    const int kt = t * kTileKeys;
+    // Waits for this wave's DMA of tile t (vmcnt) and makes every wave's
+    // writes visible; also guarantees stage (t+1)&1 is no longer being read.
     __syncthreads();
-    if (t + 1 < ntiles) load_tile(kt + kBlockN);
+    if (t + 1 < ntiles) issue_tile(kt + kTileKeys, (t + 1) & 1);
+    const uint8_t* k_stage = lds + (t & 1) * 2 * Geo::TILE_BYTES;
+    const uint8_t* v_stage = k_stage + Geo::TILE_BYTES;
 
-    // S^T for the two 32-key halves of the tile.
-    f32x16 s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x16{};
+    for (int sub = 0; sub < kTileKeys / kSubKeys; ++sub) {
+      const int rb = sub * kSubKeys;  // tile-relative first key of this step
+      const int key0 = kt + rb;
+
+      // S^T for the 32 keys x (32 * QB) queries of this wave.
+      f32x16 s[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) s[qb] = f32x16{};
 #pragma unroll
       for (int c = 0; c < QC; ++c) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(&k_lds[(32 * kb + lr) * KROW + 16 * c + 8 * hf]);
-        s[kb] = Op::mma(a, qf[c], s[kb]);
+        const u32x4 a = *reinterpret_cast<const u32x4*>(k_stage + Geo::offset(rb + lr, 2 * c + hf));
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) s[qb] = Op::mma(a, qf[qb][c], s[qb]);
       }
-    }
 
-    // Scaled logits, masking, tile max.
-    bool need_mask = kt + kBlockN > p.kv_tokens;
-    if (CAUSAL)
-      need_mask = need_mask ||
-                  (p.kv_local_offset + kt + kBlockN - 1 > p.q_local_offset + qw0 + p.causal_shift);
-    float x[2][16];
-    float mx = -INFINITY;
+      if (!scale_pos) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float val = s[kb][i] * p.scale_log2;
-        if (need_mask) {
-          const int key = kt + 32 * kb + c_row(i, hf);
-          bool ok = key < p.kv_tokens;
-          if (CAUSAL) ok = ok && (p.kv_local_offset + key <= p.q_local_offset + qi + p.causal_shift);
-          val = ok ? val : -INFINITY;
-        }
-        x[kb][i] = val;
-        mx = fmaxf(mx, val);
+        for (int qb = 0; qb < QB; ++qb) s[qb] *= p.scale_log2;
       }
-    }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_run, mx);
-    const bool row_ok = m_new != -INFINITY;
-    const float alpha = row_ok ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
-    const float m_use = row_ok ? m_new : 0.f;
-
-    // P^T (as PV B operands) and its row sum.
-    float psum = 0.f;
-    u32x4 pf[4];
+      bool need_mask = key0 + kSubKeys > p.kv_tokens;
+      if (CAUSAL)
+        need_mask = need_mask || (p.kv_local_offset + key0 + kSubKeys - 1 >
+                                  p.q_local_offset + qw0 + p.causal_shift);
+      if (need_mask) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+        for (int qb = 0; qb < QB; ++qb) {
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = __builtin_amdgcn_exp2f(x[kb][8 * half + 2 * e] - m_use);
-          const float p1 = __builtin_amdgcn_exp2f(x[kb][8 * half + 2 * e + 1] - m_use);
-          psum += p0 + p1;
-          pf[2 * kb + half][e] = Op::pack2(p0, p1);
+          for (int i = 0; i < 16; ++i) {
+            const int key = key0 + c_row(i, hf);
+            bool ok = key < p.kv_tokens;
+            if (CAUSAL) ok = ok && (p.kv_local_offset + key <= p.q_local_offset + qi[qb] + p.causal_shift);
+            s[qb][i] = ok ? s[qb][i] : -INFINITY;
+          }
         }
       }
-    }
-    psum += __shfl_xor(psum, 32);
-    l_run = l_run * alpha + psum;
-    m_run = row_ok ? m_new : m_run;
 
-    // O^T = O^T * alpha + V^T P^T.
+      // Half-row maxima (this lane's 16 keys) in the scaled domain.
+      float mx[QB];
+      bool grow = false;
 #pragma unroll
-    for (int b = 0; b < DB; ++b) {
-      acc[b] *= alpha;
-      const uint16_t* vrow = &vt_lds[(32 * b + lr) * VROW + 4 * hf];
+      for (int qb = 0; qb < QB; ++qb) {
+        float a = fmaxf(fmaxf(s[qb][0], s[qb][1]), s[qb][2]);
 #pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
-        const u32x2 a0 = *reinterpret_cast<const u32x2*>(vrow + 16 * kc);
-        const u32x2 a1 = *reinterpret_cast<const u32x2*>(vrow + 16 * kc + 8);
-        const u32x4 a = {a0[0], a0[1], a1[0], a1[1]};
-        acc[b] = Op::mma(a, pf[kc], acc[b]);
+        for (int i = 3; i < 15; i += 2) a = fmaxf(fmaxf(a, s[qb][i]), s[qb][i + 1]);
+        a = fmaxf(a, s[qb][15]);
+        mx[qb] = a * cf;
+        grow = grow || (mx[qb] > m_run[qb] + kRescaleThreshold);
+      }
+      // Rescale only when some logit of the wave left the [.., m + 8] window.
+      if (__ballot(grow) != 0) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float full = fmaxf(mx[qb], __shfl_xor(mx[qb], 32));
+          const float m_new = fmaxf(m_run[qb], full);
+          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+          l_part[qb] *= alpha;
+#pragma unroll
+          for (int d = 0; d < DB; ++d) acc[qb][d] *= alpha;
+          m_run[qb] = m_new;
+        }
+      }
+
+      // P^T (B operands of PV) and the partial row sums.
+      u32x4 pf[QB][2];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        const float neg_m = m_run[qb] == -INFINITY ? 0.f : -m_run[qb];
+        float sum = 0.f;
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][8 * kc + 2 * e], cf, neg_m));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][8 * kc + 2 * e + 1], cf, neg_m));
+            sum += p0 + p1;
+            pf[qb][kc][e] = Op::pack2(p0, p1);
+          }
+        }
+        l_part[qb] += sum;
+      }
+
+      // O^T += V^T P^T; each V^T fragment (two transposing LDS reads) feeds QB MFMAs.
+      const int grp = lane >> 4;
+      const int gi = lane & 15;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        const int granule = 4 * d + 2 * (grp & 1) + ((gi & 3) >> 1);
+#pragma unroll
+        for (int kc = 0; kc < 2; ++kc) {
+          u32x4 a;
+#pragma unroll
+          for (int r = 0; r < 2; ++r) {
+            const int row = rb + 16 * kc + 8 * r + 4 * (grp >> 1) + (gi >> 2);
+            const SA_LDS bf16x4* src = (const SA_LDS bf16x4*)(
+                (const SA_LDS uint8_t*)(v_stage) + Geo::offset(row, granule) + 8 * (gi & 1));
+            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
+                                                          const_cast<SA_LDS bf16x4*>(src)));
+            a[2 * r] = w[0];
+            a[2 * r + 1] = w[1];
+          }
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) acc[qb][d] = Op::mma(a, pf[qb][kc], acc[qb][d]);
+        }
       }
     }
   }
 
-  if (q_ok) {
-    if (hf == 0) {
-      p.m[srow] = m_run;
-      p.l[srow] = l_run;
-    }
 #pragma unroll
-    for (int b = 0; b < DB; ++b) {
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l_full = l_part[qb] + __shfl_xor(l_part[qb], 32);
+    if (qi[qb] >= p.q_tokens) continue;
+    const int64_t srow = (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+    if (hf == 0) {
+      p.m[srow] = m_run[qb];
+      p.l[srow] = l_full;
+    }
+    float* arow = p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int d = 32 * b + 8 * g + 4 * hf;
-        if (d < p.head_dim) {
-          const f32x4 v4 = {acc[b][4 * g + 0], acc[b][4 * g + 1], acc[b][4 * g + 2], acc[b][4 * g + 3]};
-          *reinterpret_cast<f32x4*>(arow + d) = v4;
+        const int col = 32 * d + 8 * g + 4 * hf;
+        if (col < p.head_dim) {
+          const f32x4 v4 = {acc[qb][d][4 * g + 0], acc[qb][d][4 * g + 1], acc[qb][d][4 * g + 2],
+                            acc[qb][d][4 * g + 3]};
+          *reinterpret_cast<f32x4*>(arow + col) = v4;
         }
       }
     }
@@ -372,7 +429,12 @@ __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
 }
 
 template <typename Op, int DP>
-hipError_t launch_update_dp(const UpdateParams& p, bool causal, bool init, dim3 grid, hipStream_t s) {
+hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t s) {
+  using Geo = Geometry<DP>;
+  p.q_blocks = (p.q_tokens + Geo::BLOCK_M - 1) / Geo::BLOCK_M;
+  const int64_t total = (int64_t)p.q_blocks * p.q_heads;
+  p.xcd_run = (int32_t)((total + 7) / 8);
+  const dim3 grid((unsigned)(8 * (int64_t)p.xcd_run));
   if (causal) {
     if (init)
       hipLaunchKernelGGL((update_kernel<Op, DP, true, true>), grid, dim3(kThreads), 0, s, p);
@@ -388,13 +450,12 @@ hipError_t launch_update_dp(const UpdateParams& p, bool causal, bool init, dim3 
 }
 
 template <typename Op>
-hipError_t launch_update_op(const UpdateParams& p, int dp, bool causal, bool init, dim3 grid,
-                            hipStream_t s) {
+hipError_t launch_update_op(const UpdateParams& p, int dp, bool causal, bool init, hipStream_t s) {
   switch (dp) {
-    case 32: return launch_update_dp<Op, 32>(p, causal, init, grid, s);
-    case 64: return launch_update_dp<Op, 64>(p, causal, init, grid, s);
-    case 128: return launch_update_dp<Op, 128>(p, causal, init, grid, s);
-    default: return launch_update_dp<Op, 256>(p, causal, init, grid, s);
+    case 32: return launch_update_dp<Op, 32>(p, causal, init, s);
+    case 64: return launch_update_dp<Op, 64>(p, causal, init, s);
+    case 128: return launch_update_dp<Op, 128>(p, causal, init, s);
+    default: return launch_update_dp<Op, 256>(p, causal, init, s);
   }
 }
 
@@ -461,11 +522,11 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
   p.causal_shift = causal_shift;
   p.scale_log2 = (float)(softmax_scale * 1.4426950408889634);
   const int dp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
-  const dim3 grid((q_tokens + kBlockM - 1) / kBlockM, q_heads);
+  p.q_heads = q_heads;
   const bool causal = (flags & SA_FLAG_CAUSAL) != 0;
   const bool init = (flags & SA_FLAG_INITIALIZE) != 0;
-  hipError_t err = dtype == SA_DTYPE_BF16 ? launch_update_op<BF16>(p, dp, causal, init, grid, stream)
-                                          : launch_update_op<FP16>(p, dp, causal, init, grid, stream);
+  hipError_t err = dtype == SA_DTYPE_BF16 ? launch_update_op<BF16>(p, dp, causal, init, stream)
+                                          : launch_update_op<FP16>(p, dp, causal, init, stream);
   return err == hipSuccess ? 0 : hip_status(err, "update kernel launch");
 }
 
