@@ -34,6 +34,11 @@ HIP_FLAGS = [
     "-target-feature",
     "-Xclang",
     "-packed-fp32-ops",
+    # Keep MFMA accumulators in VGPRs: the softmax rescale multiplies them
+    # with VALU ops, and AGPR-resident accumulators were copied to VGPRs and
+    # back on every tile.
+    "-mllvm",
+    "--amdgpu-mfma-vgpr-form",
 ]
 
 

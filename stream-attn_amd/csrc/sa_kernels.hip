@@ -221,26 +221,42 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
   const bool scale_pos = p.scale_log2 > 0.f;
   const float cf = scale_pos ? p.scale_log2 : 1.f;
 
-  // HBM/L2 -> LDS DMA of key tile [kt, kt + 64) into stage st.  Rows past the
-  // chunk are clamped to its last row and granules past head_dim to granule 0:
-  // those values are finite, masked (keys) or multiplied by zero Q / never
-  // stored (d), and every address stays inside the caller's buffers.
+  // HBM/L2 -> LDS DMA of key tile [kt, kt + 64) into stage st.  Each lane's
+  // element offset within a tile is fixed (precomputed below); the tile base
+  // is wave-uniform.  In the tail tile, rows past the chunk are clamped to its
+  // last row, and granules past head_dim always read granule 0: those values
+  // are finite and masked (keys) or multiplied by zero Q / never stored (d),
+  // and every address stays inside the caller's buffers.
+  int k_off[Geo::DMA_PER_WAVE], v_off[Geo::DMA_PER_WAVE], dma_row[Geo::DMA_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
+    const int chunk = wave * Geo::DMA_PER_WAVE + i;
+    const int row = chunk * Geo::ROWS_PER_DMA + lane / G;
+    const int lg = (lane % G) ^ Geo::swz(row);
+    const int col = (lg * 8 < p.head_dim) ? lg * 8 : 0;
+    dma_row[i] = row;
+    k_off[i] = row * (int)p.sk_t + col;
+    v_off[i] = row * (int)p.sv_t + col;
+  }
   auto issue_tile = [&](int kt, int st) {
     uint8_t* k_stage = lds + st * 2 * Geo::TILE_BYTES;
     uint8_t* v_stage = k_stage + Geo::TILE_BYTES;
+    const uint16_t* kt_base = kp + (int64_t)kt * p.sk_t;
+    const uint16_t* vt_base = vp + (int64_t)kt * p.sv_t;
+    const bool tail = kt + kTileKeys > p.kv_tokens;
 #pragma unroll
     for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
       const int chunk = wave * Geo::DMA_PER_WAVE + i;
-      const int row = chunk * Geo::ROWS_PER_DMA + lane / G;
-      const int lg = (lane % G) ^ Geo::swz(row);
-      const int grow = min(kt + row, p.kv_tokens - 1);
-      const int col = (lg * 8 < p.head_dim) ? lg * 8 : 0;
-      __builtin_amdgcn_global_load_lds(
-          (const SA_GLOBAL void*)(kp + (int64_t)grow * p.sk_t + col),
-          (SA_LDS void*)(k_stage + chunk * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(
-          (const SA_GLOBAL void*)(vp + (int64_t)grow * p.sv_t + col),
-          (SA_LDS void*)(v_stage + chunk * 1024), 16, 0, 0);
+      int ko = k_off[i], vo = v_off[i];
+      if (tail && kt + dma_row[i] >= p.kv_tokens) {
+        const int back = kt + dma_row[i] - (p.kv_tokens - 1);  // rows to step back
+        ko -= back * (int)p.sk_t;
+        vo -= back * (int)p.sv_t;
+      }
+      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kt_base + ko),
+                                       (SA_LDS void*)(k_stage + chunk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(vt_base + vo),
+                                       (SA_LDS void*)(v_stage + chunk * 1024), 16, 0, 0);
     }
   };
 
@@ -498,6 +514,11 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
       set_error("sa_update_attention_state: q/k/v token and head strides must be multiples of 8 elements");
       return SA_ERR_INVALID_ARGUMENT;
     }
+  }
+  if (sk_t <= 0 || sv_t <= 0 || sk_t >= (1 << 24) || sv_t >= (1 << 24)) {
+    // Per-lane offsets within a 64-key tile are 32-bit.
+    set_error("sa_update_attention_state: k/v token strides must be in [1, 2^24) elements");
+    return SA_ERR_INVALID_ARGUMENT;
   }
   if (sa_t % 4 != 0 || sa_h % 4 != 0 || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) ||
       !aligned(acc, 16) || !aligned(m, 4) || !aligned(l, 4)) {
