@@ -136,7 +136,12 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
   constexpr int DB = DP / 32;  // 32-row d blocks of the PV output
   constexpr int G = Geo::G;
 
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[2 * 2 * Geo::TILE_BYTES];
+  // Two LDS stages as distinct objects: every LDS read and every DMA target
+  // below names one of them statically, so the compiler can tell that the
+  // in-flight prefetch into one stage does not alias reads of the other and
+  // need not wait for it.
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[2 * Geo::TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b[2 * Geo::TILE_BYTES];
 
   // XCD-aware numbering: hardware block b runs on XCD b % 8; consecutive
   // logical workgroups (same head, neighbouring query blocks) share an XCD.
@@ -238,9 +243,9 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
     k_off[i] = row * (int)p.sk_t + col;
     v_off[i] = row * (int)p.sv_t + col;
   }
-  auto issue_tile = [&](int kt, int st) {
-    uint8_t* k_stage = lds + st * 2 * Geo::TILE_BYTES;
-    uint8_t* v_stage = k_stage + Geo::TILE_BYTES;
+  auto issue_tile = [&](int kt, uint8_t* stage) {
+    uint8_t* k_stage = stage;
+    uint8_t* v_stage = stage + Geo::TILE_BYTES;
     const uint16_t* kt_base = kp + (int64_t)kt * p.sk_t;
     const uint16_t* vt_base = vp + (int64_t)kt * p.sv_t;
     const bool tail = kt + kTileKeys > p.kv_tokens;
@@ -260,31 +265,35 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
     }
   };
 
-  if (ntiles > 0) issue_tile(0, 0);
-
-  for (int t = 0; t < ntiles; ++t) {
+  // Tile t is computed from `cur` while tile t+1 streams into `next`.
+  auto tile = [&](int t, const uint8_t* cur, uint8_t* next) {
     const int kt = t * kTileKeys;
     // Waits for this wave's DMA of tile t (vmcnt) and makes every wave's
-    // writes visible; also guarantees stage (t+1)&1 is no longer being read.
+    // writes visible; also guarantees `next` is no longer being read.
     __syncthreads();
-    if (t + 1 < ntiles) issue_tile(kt + kTileKeys, (t + 1) & 1);
-    const uint8_t* k_stage = lds + (t & 1) * 2 * Geo::TILE_BYTES;
-    const uint8_t* v_stage = k_stage + Geo::TILE_BYTES;
+    if (t + 1 < ntiles) issue_tile(kt + kTileKeys, next);
+    const uint8_t* k_stage = cur;
+    const uint8_t* v_stage = cur + Geo::TILE_BYTES;
 
 #pragma unroll
     for (int sub = 0; sub < kTileKeys / kSubKeys; ++sub) {
       const int rb = sub * kSubKeys;  // tile-relative first key of this step
       const int key0 = kt + rb;
 
-      // S^T for the 32 keys x (32 * QB) queries of this wave.
+      // S^T for the 32 keys x (32 * QB) queries of this wave.  All K
+      // fragments of the step are requested before the first MFMA so the
+      // LDS latency is paid once.
+      u32x4 kf[QC];
+#pragma unroll
+      for (int c = 0; c < QC; ++c)
+        kf[c] = *reinterpret_cast<const u32x4*>(k_stage + Geo::offset(rb + lr, 2 * c + hf));
       f32x16 s[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) s[qb] = f32x16{};
 #pragma unroll
       for (int c = 0; c < QC; ++c) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(k_stage + Geo::offset(rb + lr, 2 * c + hf));
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[qb] = Op::mma(a, qf[qb][c], s[qb]);
+        for (int qb = 0; qb < QB; ++qb) s[qb] = Op::mma(kf[c], qf[qb][c], s[qb]);
       }
 
       if (!scale_pos) {
@@ -353,30 +362,59 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
         l_part[qb] += sum;
       }
 
-      // O^T += V^T P^T; each V^T fragment (two transposing LDS reads) feeds QB MFMAs.
+      // O^T += V^T P^T; each V^T fragment (two transposing LDS reads) feeds QB
+      // MFMAs.  The reads of a batch of up to 4 d-blocks are all issued before
+      // the batch's MFMAs.  They are inline asm followed by one explicit
+      // lgkmcnt wait: the compiler cannot relate a transposing LDS read to the
+      // DMA writing the other stage and would otherwise wait for that prefetch
+      // (vmcnt) before every read.  LDS reads complete in order, so the
+      // compiler's own lgkmcnt waits around these remain sufficient.
       const int grp = lane >> 4;
       const int gi = lane & 15;
+      const uint32_t v_lds = (uint32_t)(uintptr_t)(const SA_LDS uint8_t*)(v_stage);
+      constexpr int VB = DB < 4 ? DB : 4;
 #pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        const int granule = 4 * d + 2 * (grp & 1) + ((gi & 3) >> 1);
+      for (int d0 = 0; d0 < DB; d0 += VB) {
+        u32x4 vf[VB][2];
 #pragma unroll
-        for (int kc = 0; kc < 2; ++kc) {
-          u32x4 a;
+        for (int dd = 0; dd < VB; ++dd) {
+          const int granule = 4 * (d0 + dd) + 2 * (grp & 1) + ((gi & 3) >> 1);
 #pragma unroll
-          for (int r = 0; r < 2; ++r) {
-            const int row = rb + 16 * kc + 8 * r + 4 * (grp >> 1) + (gi >> 2);
-            const SA_LDS bf16x4* src = (const SA_LDS bf16x4*)(
-                (const SA_LDS uint8_t*)(v_stage) + Geo::offset(row, granule) + 8 * (gi & 1));
-            const u32x2 w = __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(
-                                                          const_cast<SA_LDS bf16x4*>(src)));
-            a[2 * r] = w[0];
-            a[2 * r + 1] = w[1];
+          for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+              const int row = rb + 16 * kc + 8 * r + 4 * (grp >> 1) + (gi >> 2);
+              const uint32_t addr = v_lds + Geo::offset(row, granule) + 8 * (gi & 1);
+              u32x2 w;
+              asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(addr));
+              vf[dd][kc][2 * r] = w[0];
+              vf[dd][kc][2 * r + 1] = w[1];
+            }
           }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-          for (int qb = 0; qb < QB; ++qb) acc[qb][d] = Op::mma(a, pf[qb][kc], acc[qb][d]);
+        for (int dd = 0; dd < VB; ++dd) {
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) asm volatile("" : "+v"(vf[dd][kc]));
+        }
+#pragma unroll
+        for (int dd = 0; dd < VB; ++dd) {
+#pragma unroll
+          for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+            for (int qb = 0; qb < QB; ++qb)
+              acc[qb][d0 + dd] = Op::mma(vf[dd][kc], pf[qb][kc], acc[qb][d0 + dd]);
+          }
         }
       }
     }
+  };
+
+  if (ntiles > 0) issue_tile(0, lds_a);
+  for (int t = 0; t < ntiles; t += 2) {
+    tile(t, lds_a, lds_b);
+    if (t + 1 < ntiles) tile(t + 1, lds_b, lds_a);
   }
 
 #pragma unroll
