@@ -196,6 +196,65 @@ int32_t sa_pipeline_stream_kv(sa_pipeline* pipeline, const void* k_host, const v
                               void* compute_stream, sa_pipeline_stats* stats);
 
 /*
+ * Stream one contiguous K/V span of a segment: host rows k_host/v_host hold
+ * segment positions [kv_local_offset, kv_local_offset + kv_tokens).  The span
+ * goes through the ring in chunks of at most kv_chunk_tokens rows and every
+ * chunk updates the resident Q block.  Paged mode coalesces consecutive
+ * pages of a segment into one span (replaces the per-page loop of
+ * paged/runtime/triton.py:109-238, whose kernel launches cover one page each).
+ * *initialize: in, nonzero while the state still has to be defined by the
+ * next launch (the first span of a Q block); out, 0 once a launch did.  With
+ * kv_tokens == 0 and *initialize set, the state is initialized to "no keys".
+ * Ring slots rotate across calls; the H2D copies are on the pipeline's H2D
+ * stream, so an event recorded there after this call marks the host rows as
+ * consumed.
+ */
+int32_t sa_pipeline_stream_kv_span(sa_pipeline* pipeline, const void* k_host, const void* v_host,
+                                   int32_t kv_tokens, int32_t kv_local_offset,
+                                   int32_t* initialize, int32_t q_tokens,
+                                   int32_t q_local_offset, int32_t causal_shift,
+                                   double softmax_scale, int32_t causal, void* compute_stream,
+                                   sa_pipeline_stats* stats);
+
+/*
+ * Gathered form of sa_pipeline_stream_kv_span for paged sources: the span's
+ * host rows are split over num_fragments contiguous fragments (one per
+ * page: K rows k_fragments[i], V rows v_fragments[i], fragment_tokens[i]
+ * rows each), in segment order starting at kv_local_offset.  Fragments are
+ * packed into ring slots of up to kv_chunk_tokens rows with one H2D copy per
+ * piece, and each slot is one update launch (the reference copies a page
+ * into a pinned stage and launches per page, paged/runtime/triton.py:119-238).
+ * Fragment memory must stay valid and unmodified until an event recorded on
+ * the H2D stream after this call has completed.
+ */
+int32_t sa_pipeline_stream_kv_gather(sa_pipeline* pipeline, const void* const* k_fragments,
+                                     const void* const* v_fragments,
+                                     const int32_t* fragment_tokens, int32_t num_fragments,
+                                     int32_t kv_local_offset, int32_t* initialize,
+                                     int32_t q_tokens, int32_t q_local_offset,
+                                     int32_t causal_shift, double softmax_scale, int32_t causal,
+                                     void* compute_stream, sa_pipeline_stats* stats);
+
+/*
+ * HBM-resident execution: Q/K/V and out are device tensors (strides in
+ * elements, unit stride over head_dim), so nothing crosses PCIe.  Same Q
+ * super-block / K/V chunk decomposition as sa_pipeline_run, using the
+ * pipeline's state buffers; K/V chunks and Q blocks are read in place and
+ * each block is finalized straight into out (and lse when non-NULL, layout
+ * [q_heads, total_q] with row stride lse_stride_h).  Enqueued on
+ * compute_stream; returns without waiting.  The reference accepts host
+ * tensors only (validation.py:13-14); this is the device-input extension.
+ */
+int32_t sa_pipeline_run_resident(sa_pipeline* pipeline, const void* q, const void* k,
+                                 const void* v, void* out, float* lse, int64_t stride_qt,
+                                 int64_t stride_qh, int64_t stride_kt, int64_t stride_kh,
+                                 int64_t stride_vt, int64_t stride_vh, int64_t stride_ot,
+                                 int64_t stride_oh, int64_t lse_stride_h,
+                                 const int64_t* cu_seqlens_q, const int64_t* cu_seqlens_k,
+                                 int32_t num_segments, double softmax_scale, int32_t causal,
+                                 void* compute_stream, sa_pipeline_stats* stats);
+
+/*
  * Finalize the resident state on compute_stream (executor.py:125-142).
  * slot >= 0: into output slot `slot`; the Q-free event is recorded first (the
  * next Q H2D may start) and finalize waits for the slot's previous D2H.

@@ -268,8 +268,12 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
   // Tile t is computed from `cur` while tile t+1 streams into `next`.
   auto tile = [&](int t, const uint8_t* cur, uint8_t* next) {
     const int kt = t * kTileKeys;
-    // Waits for this wave's DMA of tile t (vmcnt) and makes every wave's
-    // writes visible; also guarantees `next` is no longer being read.
+    // Every wave waits for its own DMA of tile t before the barrier, so after
+    // it all 64 rows of `cur` are in LDS.  LDS DMA is counted by vmcnt, which
+    // a workgroup-scope fence does not wait for: without this explicit wait a
+    // wave could read rows that another wave's DMA has not written yet.  The
+    // barrier also guarantees `next` (tile t-1) is no longer being read.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (t + 1 < ntiles) issue_tile(kt + kTileKeys, next);
     const uint8_t* k_stage = cur;

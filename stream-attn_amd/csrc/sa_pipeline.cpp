@@ -18,6 +18,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <new>
 #include <cstdarg>
 #include <cstdio>
@@ -75,6 +76,7 @@ struct sa_pipeline {
   bool q_pending = false;
   bool kv_pending[3] = {false, false, false};
   bool out_pending[2] = {false, false};
+  int64_t ring_next = 0;  // next K/V ring slot (rotates across calls)
 
   // Optional timing of update launches (event pairs on the compute stream).
   bool timing = false;
@@ -132,6 +134,178 @@ int32_t load_q(sa_pipeline* p, const void* q_host, int32_t q_tokens, hipStream_t
   return 0;
 }
 
+// One update launch over rows [start, start + n) of a K/V span, optionally
+// bracketed by timing events.
+int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, const void* k,
+                     int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_t, int64_t sv_h,
+                     int32_t q_tokens, int32_t kv_tokens, int32_t q_local_offset,
+                     int32_t kv_local_offset, int32_t causal_shift, double scale, int32_t flags,
+                     hipStream_t compute) {
+  if (p->timing) {
+    if (p->t_used == p->t_start.size()) {
+      hipEvent_t a = nullptr, b = nullptr;
+      SA_HIP_RETURN(hipEventCreate(&a));
+      SA_HIP_RETURN(hipEventCreate(&b));
+      p->t_start.push_back(a);
+      p->t_stop.push_back(b);
+    }
+    SA_HIP_RETURN(hipEventRecord(p->t_start[p->t_used], compute));
+  }
+  const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+  int32_t rc = sa::launch_update(q, k, v, p->m, p->l, p->acc, sq_t, sq_h, sk_t, sk_h, sv_t, sv_h,
+                                 p->q_heads, 1, qt, p->head_dim, q_tokens, kv_tokens, p->q_heads,
+                                 p->kv_heads, p->head_dim, q_local_offset, kv_local_offset,
+                                 causal_shift, scale, flags, p->dtype, compute);
+  if (rc != 0) return rc;
+  if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
+  return 0;
+}
+
+// Where the K/V rows of a span live: pinned host rows copied through the ring
+// (tensor and paged modes), or device rows read in place (HBM-resident mode).
+struct KVSource {
+  const char* k;
+  const char* v;
+  bool on_device;
+  int64_t sk_t, sk_h, sv_t, sv_h;  // element strides, used when on_device
+};
+
+// Apply K/V rows [kv_local_offset, kv_local_offset + kv_tokens) of one segment
+// to the resident Q block, kv_chunk_tokens rows per launch.  `initialize` is
+// true while the state still has to be defined by the next launch; it is
+// cleared by the first launch.  Keys at or beyond `visible_end` are masked for
+// every query of the block under the bottom-right causal rule; their chunks
+// change nothing and are neither copied nor launched, except that a chunk
+// always runs while the state is uninitialized.
+int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, const KVSource& src,
+                   int32_t kv_tokens, int32_t kv_local_offset, bool* initialize,
+                   int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
+                   int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
+  if (kv_tokens < 0 || kv_local_offset < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
+    sa::set_error("bad K/V span kv_tokens=%d kv_local_offset=%d q_tokens=%d", kv_tokens,
+                  kv_local_offset, q_tokens);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  int64_t visible_end = INT64_MAX;
+  if (causal) visible_end = std::max<int64_t>(0, (int64_t)q_local_offset + q_tokens + causal_shift);
+  const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+  for (int32_t start = 0; start < kv_tokens; start += p->kv_chunk) {
+    const int64_t position = (int64_t)kv_local_offset + start;
+    if (!*initialize && position >= visible_end) break;
+    const int32_t n = std::min(p->kv_chunk, kv_tokens - start);
+    const int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (*initialize ? SA_FLAG_INITIALIZE : 0);
+    int32_t rc;
+    if (src.on_device) {
+      rc = launch_timed(p, q, sq_t, sq_h, src.k + start * src.sk_t * 2, src.sk_t, src.sk_h,
+                        src.v + start * src.sv_t * 2, src.sv_t, src.sv_h, q_tokens, n,
+                        q_local_offset, (int32_t)position, causal_shift, scale, flags, compute);
+      if (rc != 0) return rc;
+      add_stats(st, 0, 0, 0, 1, 0);
+    } else {
+      const int slot = (int)(p->ring_next++ % p->num_kv);
+      const int64_t bytes = (int64_t)n * p->kv_row_bytes;
+      if (p->kv_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free[slot], 0));
+      SA_HIP_RETURN(hipMemcpyAsync(p->k_slots[slot], src.k + (int64_t)start * p->kv_row_bytes,
+                                   bytes, hipMemcpyHostToDevice, p->h2d));
+      SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], src.v + (int64_t)start * p->kv_row_bytes,
+                                   bytes, hipMemcpyHostToDevice, p->h2d));
+      SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
+      add_stats(st, 2 * bytes, 0, 0, 1, 0);
+      SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
+      rc = launch_timed(p, q, sq_t, sq_h, p->k_slots[slot], kt, p->head_dim, p->v_slots[slot], kt,
+                        p->head_dim, q_tokens, n, q_local_offset, (int32_t)position, causal_shift,
+                        scale, flags, compute);
+      if (rc != 0) return rc;
+      SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
+      p->kv_pending[slot] = true;
+    }
+    *initialize = false;
+  }
+  return 0;
+}
+
+// Gathered span: consecutive segment positions [kv_local_offset, +total)
+// whose host rows are split over `nfrag` contiguous fragments (one per page).
+// Ring slots are filled fragment piece by fragment piece (one hipMemcpyAsync
+// per piece and tensor), so page-sized host records feed chunk-sized kernel
+// launches without a host-side copy.
+int32_t apply_gather(sa_pipeline* p, const void* const* k_frags, const void* const* v_frags,
+                     const int32_t* frag_tokens, int32_t nfrag, int32_t kv_local_offset,
+                     bool* initialize, int32_t q_tokens, int32_t q_local_offset,
+                     int32_t causal_shift, double scale, int32_t causal, hipStream_t compute,
+                     sa_pipeline_stats* st) {
+  int64_t total = 0;
+  for (int32_t i = 0; i < nfrag; ++i) {
+    if (frag_tokens[i] < 0 || (frag_tokens[i] > 0 && (!k_frags[i] || !v_frags[i]))) {
+      sa::set_error("bad K/V fragment %d (%d tokens)", i, frag_tokens[i]);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    total += frag_tokens[i];
+  }
+  if (total > INT32_MAX || kv_local_offset < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
+    sa::set_error("bad gathered K/V span (%lld tokens at %d, q_tokens %d)", (long long)total,
+                  kv_local_offset, q_tokens);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  int64_t visible_end = INT64_MAX;
+  if (causal) visible_end = std::max<int64_t>(0, (int64_t)q_local_offset + q_tokens + causal_shift);
+  const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+  const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+  int32_t frag = 0;       // fragment holding the next row
+  int64_t frag_row = 0;   // rows of that fragment already consumed
+  for (int64_t start = 0; start < total; start += p->kv_chunk) {
+    const int64_t position = (int64_t)kv_local_offset + start;
+    if (!*initialize && position >= visible_end) break;
+    const int32_t n = (int32_t)std::min<int64_t>(p->kv_chunk, total - start);
+    const int slot = (int)(p->ring_next++ % p->num_kv);
+    if (p->kv_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free[slot], 0));
+    char* kd = static_cast<char*>(p->k_slots[slot]);
+    char* vd = static_cast<char*>(p->v_slots[slot]);
+    int64_t filled = 0;
+    while (filled < n) {
+      while (frag < nfrag && frag_row >= frag_tokens[frag]) {
+        ++frag;
+        frag_row = 0;
+      }
+      const int64_t rows = std::min<int64_t>(n - filled, frag_tokens[frag] - frag_row);
+      const int64_t bytes = rows * p->kv_row_bytes;
+      const int64_t src_off = frag_row * p->kv_row_bytes;
+      SA_HIP_RETURN(hipMemcpyAsync(kd + filled * p->kv_row_bytes,
+                                   static_cast<const char*>(k_frags[frag]) + src_off, bytes,
+                                   hipMemcpyHostToDevice, p->h2d));
+      SA_HIP_RETURN(hipMemcpyAsync(vd + filled * p->kv_row_bytes,
+                                   static_cast<const char*>(v_frags[frag]) + src_off, bytes,
+                                   hipMemcpyHostToDevice, p->h2d));
+      filled += rows;
+      frag_row += rows;
+    }
+    SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
+    add_stats(st, 2 * (int64_t)n * p->kv_row_bytes, 0, 0, 1, 0);
+    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
+    const int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (*initialize ? SA_FLAG_INITIALIZE : 0);
+    int32_t rc = launch_timed(p, p->q_buffer, qt, p->head_dim, kd, kt, p->head_dim, vd, kt,
+                              p->head_dim, q_tokens, n, q_local_offset, (int32_t)position,
+                              causal_shift, scale, flags, compute);
+    if (rc != 0) return rc;
+    SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
+    p->kv_pending[slot] = true;
+    *initialize = false;
+  }
+  return 0;
+}
+
+// Defines the state of a Q block that sees no keys at all (m = -inf, l = 0,
+// acc = 0): an update launch with zero keys and the initialize flag.
+int32_t init_state(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, int32_t q_tokens,
+                   int32_t q_local_offset, int32_t causal_shift, double scale,
+                   hipStream_t compute) {
+  if (q_tokens <= 0) return 0;
+  const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+  return launch_timed(p, q, sq_t, sq_h, p->k_slots[0], kt, p->head_dim, p->v_slots[0], kt,
+                      p->head_dim, q_tokens, 0, q_local_offset, 0, causal_shift, scale,
+                      SA_FLAG_INITIALIZE, compute);
+}
+
 int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_t k_length,
                   int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
                   int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
@@ -139,67 +313,15 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
     sa::set_error("bad stream_kv sizes k_length=%d q_tokens=%d", k_length, q_tokens);
     return SA_ERR_INVALID_ARGUMENT;
   }
-  const char* kh = static_cast<const char*>(k_host);
-  const char* vh = static_cast<const char*>(v_host);
-  // Keys at or beyond `visible_end` are masked for every query of the block
-  // under the bottom-right causal rule; their chunks change nothing and are
-  // neither copied nor launched (the first chunk always runs so the state is
-  // initialized).
-  int64_t visible_end = k_length;
-  if (causal) {
-    visible_end = (int64_t)q_local_offset + q_tokens - 1 + causal_shift + 1;
-    visible_end = std::max<int64_t>(0, std::min<int64_t>(visible_end, k_length));
-  }
+  const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+  KVSource src{static_cast<const char*>(k_host), static_cast<const char*>(v_host), false, 0, 0, 0, 0};
   bool initialize = true;
-  int index = 0;
-  for (int32_t start = 0; start < k_length; start += p->kv_chunk, ++index) {
-    if (!initialize && start >= visible_end) break;
-    const int32_t n = std::min(p->kv_chunk, k_length - start);
-    const int slot = index % p->num_kv;
-    const int64_t bytes = (int64_t)n * p->kv_row_bytes;
-    if (p->kv_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free[slot], 0));
-    SA_HIP_RETURN(hipMemcpyAsync(p->k_slots[slot], kh + (int64_t)start * p->kv_row_bytes, bytes,
-                                 hipMemcpyHostToDevice, p->h2d));
-    SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], vh + (int64_t)start * p->kv_row_bytes, bytes,
-                                 hipMemcpyHostToDevice, p->h2d));
-    SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
-    add_stats(st, 2 * bytes, 0, 0, 1, 0);
-    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
-    const int64_t qt = (int64_t)p->q_heads * p->head_dim;
-    const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
-    int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (initialize ? SA_FLAG_INITIALIZE : 0);
-    if (p->timing) {
-      if (p->t_used == p->t_start.size()) {
-        hipEvent_t a = nullptr, b = nullptr;
-        SA_HIP_RETURN(hipEventCreate(&a));
-        SA_HIP_RETURN(hipEventCreate(&b));
-        p->t_start.push_back(a);
-        p->t_stop.push_back(b);
-      }
-      SA_HIP_RETURN(hipEventRecord(p->t_start[p->t_used], compute));
-    }
-    int32_t rc = sa::launch_update(p->q_buffer, p->k_slots[slot], p->v_slots[slot], p->m, p->l,
-                                   p->acc, qt, p->head_dim, kt, p->head_dim, kt, p->head_dim,
-                                   p->q_heads, 1, qt, p->head_dim, q_tokens, n, p->q_heads,
-                                   p->kv_heads, p->head_dim, q_local_offset, start, causal_shift,
-                                   scale, flags, p->dtype, compute);
-    if (rc != 0) return rc;
-    if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
-    initialize = false;
-    SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
-    p->kv_pending[slot] = true;
-  }
-  if (initialize && q_tokens > 0) {
-    // No keys at all: still define the state (m = -inf, l = 0, acc = 0).
-    const int64_t qt = (int64_t)p->q_heads * p->head_dim;
-    int32_t rc = sa::launch_update(p->q_buffer, p->k_slots[0], p->v_slots[0], p->m, p->l, p->acc,
-                                   qt, p->head_dim, (int64_t)p->kv_heads * p->head_dim,
-                                   p->head_dim, (int64_t)p->kv_heads * p->head_dim, p->head_dim,
-                                   p->q_heads, 1, qt, p->head_dim, q_tokens, 0, p->q_heads,
-                                   p->kv_heads, p->head_dim, q_local_offset, 0, causal_shift,
-                                   scale, SA_FLAG_INITIALIZE, p->dtype, compute);
-    if (rc != 0) return rc;
-  }
+  int32_t rc = apply_span(p, p->q_buffer, qt, p->head_dim, src, k_length, 0, &initialize,
+                          q_tokens, q_local_offset, causal_shift, scale, causal, compute, st);
+  if (rc != 0) return rc;
+  if (initialize)
+    return init_state(p, p->q_buffer, qt, p->head_dim, q_tokens, q_local_offset, causal_shift,
+                      scale, compute);
   return 0;
 }
 
@@ -387,6 +509,113 @@ int32_t sa_pipeline_stream_kv(sa_pipeline* p, const void* k_host, const void* v_
   sa::DeviceGuard guard(p->device);
   return stream_kv(p, k_host, v_host, k_length, q_tokens, q_local_offset, causal_shift,
                    softmax_scale, causal, static_cast<hipStream_t>(compute_stream), stats);
+}
+
+int32_t sa_pipeline_stream_kv_span(sa_pipeline* p, const void* k_host, const void* v_host,
+                                   int32_t kv_tokens, int32_t kv_local_offset,
+                                   int32_t* initialize, int32_t q_tokens,
+                                   int32_t q_local_offset, int32_t causal_shift,
+                                   double softmax_scale, int32_t causal, void* compute_stream,
+                                   sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p || !initialize || (kv_tokens > 0 && (!k_host || !v_host))) {
+    sa::set_error("sa_pipeline_stream_kv_span: null argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa::DeviceGuard guard(p->device);
+  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+  KVSource src{static_cast<const char*>(k_host), static_cast<const char*>(v_host), false, 0, 0, 0, 0};
+  bool init = *initialize != 0;
+  int32_t rc;
+  if (kv_tokens == 0) {
+    rc = init ? init_state(p, p->q_buffer, qt, p->head_dim, q_tokens, q_local_offset,
+                           causal_shift, softmax_scale, compute)
+              : 0;
+    init = false;
+  } else {
+    rc = apply_span(p, p->q_buffer, qt, p->head_dim, src, kv_tokens, kv_local_offset, &init,
+                    q_tokens, q_local_offset, causal_shift, softmax_scale, causal, compute, stats);
+  }
+  *initialize = init ? 1 : 0;
+  return rc;
+}
+
+int32_t sa_pipeline_stream_kv_gather(sa_pipeline* p, const void* const* k_fragments,
+                                     const void* const* v_fragments,
+                                     const int32_t* fragment_tokens, int32_t num_fragments,
+                                     int32_t kv_local_offset, int32_t* initialize,
+                                     int32_t q_tokens, int32_t q_local_offset,
+                                     int32_t causal_shift, double softmax_scale, int32_t causal,
+                                     void* compute_stream, sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p || !initialize || num_fragments < 0 ||
+      (num_fragments > 0 && (!k_fragments || !v_fragments || !fragment_tokens))) {
+    sa::set_error("sa_pipeline_stream_kv_gather: null argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa::DeviceGuard guard(p->device);
+  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  bool init = *initialize != 0;
+  int32_t rc = apply_gather(p, k_fragments, v_fragments, fragment_tokens, num_fragments,
+                            kv_local_offset, &init, q_tokens, q_local_offset, causal_shift,
+                            softmax_scale, causal, compute, stats);
+  *initialize = init ? 1 : 0;
+  return rc;
+}
+
+int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, const void* v,
+                                 void* out, float* lse, int64_t stride_qt, int64_t stride_qh,
+                                 int64_t stride_kt, int64_t stride_kh, int64_t stride_vt,
+                                 int64_t stride_vh, int64_t stride_ot, int64_t stride_oh,
+                                 int64_t lse_stride_h, const int64_t* cu_seqlens_q,
+                                 const int64_t* cu_seqlens_k, int32_t num_segments,
+                                 double softmax_scale, int32_t causal, void* compute_stream,
+                                 sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p || !q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k || num_segments < 0) {
+    sa::set_error("sa_pipeline_run_resident: null argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa::DeviceGuard guard(p->device);
+  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  const char* qd = static_cast<const char*>(q);
+  const char* kd = static_cast<const char*>(k);
+  const char* vd = static_cast<const char*>(v);
+  char* od = static_cast<char*>(out);
+  const int64_t qt_stride = (int64_t)p->q_heads * p->head_dim;
+  for (int32_t s = 0; s < num_segments; ++s) {
+    const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
+    const int64_t k_start = cu_seqlens_k[s], k_stop = cu_seqlens_k[s + 1];
+    const int64_t q_length = q_stop - q_start, k_length = k_stop - k_start;
+    if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0)) {
+      sa::set_error("sa_pipeline_run_resident: segment %d has invalid bounds", s);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    const int32_t causal_shift = (int32_t)(k_length - q_length);
+    KVSource src{kd + k_start * stride_kt * 2, vd + k_start * stride_vt * 2, true,
+                 stride_kt, stride_kh, stride_vt, stride_vh};
+    for (int64_t qs = q_start; qs < q_stop; qs += p->q_chunk) {
+      const int32_t n = (int32_t)std::min<int64_t>(p->q_chunk, q_stop - qs);
+      const char* qblock = qd + qs * stride_qt * 2;
+      bool initialize = true;
+      int32_t rc = apply_span(p, qblock, stride_qt, stride_qh, src, (int32_t)k_length, 0,
+                              &initialize, n, (int32_t)(qs - q_start), causal_shift,
+                              softmax_scale, causal, compute, stats);
+      if (rc != 0) return rc;
+      if (initialize) {
+        rc = init_state(p, qblock, stride_qt, stride_qh, n, (int32_t)(qs - q_start), causal_shift,
+                        softmax_scale, compute);
+        if (rc != 0) return rc;
+      }
+      rc = sa::launch_finalize(p->acc, p->m, p->l, od + qs * stride_ot * 2, lse, qt_stride,
+                               p->head_dim, p->q_heads, 1, stride_ot, stride_oh, lse_stride_h, qs,
+                               n, p->q_heads, p->head_dim, p->dtype, compute);
+      if (rc != 0) return rc;
+      add_stats(stats, 0, 0, 1, 0, n);
+    }
+  }
+  return 0;
 }
 
 int32_t sa_pipeline_finalize(sa_pipeline* p, int32_t slot, int32_t q_tokens, float* lse,

@@ -76,6 +76,23 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_void_p, c_void_p, c_int32, c_int32, c_int32, c_int32, c_double, c_int32,
          c_void_p, ctypes.POINTER(PipelineStats)],
     ),
+    "sa_pipeline_stream_kv_span": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_int32, c_int32, ctypes.POINTER(c_int32), c_int32, c_int32,
+         c_int32, c_double, c_int32, c_void_p, ctypes.POINTER(PipelineStats)],
+    ),
+    "sa_pipeline_stream_kv_gather": (
+        c_int32,
+        [c_void_p, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p), ctypes.POINTER(c_int32), c_int32,
+         c_int32, ctypes.POINTER(c_int32), c_int32, c_int32, c_int32, c_double, c_int32, c_void_p,
+         ctypes.POINTER(PipelineStats)],
+    ),
+    "sa_pipeline_run_resident": (
+        c_int32,
+        [c_void_p] * 6 + [c_int64] * 9
+        + [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64), c_int32, c_double, c_int32, c_void_p,
+           ctypes.POINTER(PipelineStats)],
+    ),
     "sa_pipeline_finalize": (
         c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_int64, c_int64, c_void_p]
     ),

@@ -80,6 +80,42 @@ class HipExecutorMixin:
         _merge_stats(stats, native_stats)
         return out
 
+    def _run_resident(
+        self,
+        q: torch.Tensor,
+        k: torch.Tensor,
+        v: torch.Tensor,
+        q_bounds: list[int],
+        k_bounds: list[int],
+        scale: float,
+        causal: bool,
+        out: torch.Tensor,
+        stats: StreamingAttentionStats,
+        lse: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """HBM-resident inputs and output: one native call, no PCIe traffic.
+
+        Enqueued on the runner's compute stream (torch's current stream at
+        construction); the caller synchronizes as with any torch op.
+        """
+        workspace = self._workspace
+        self._check_lse(lse, q.shape[0])
+        native_stats = _native.PipelineStats()
+        with torch.cuda.device(self.plan.device), self._range("seqattn:run_resident"):
+            status = _native.lib().sa_pipeline_run_resident(
+                workspace.handle,
+                q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(),
+                None if lse is None else lse.data_ptr(),
+                q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+                out.stride(0), out.stride(1), 0 if lse is None else lse.stride(0),
+                _bounds_array(q_bounds), _bounds_array(k_bounds), len(q_bounds) - 1,
+                float(scale), int(bool(causal)),
+                workspace.compute_stream.cuda_stream, ctypes.byref(native_stats),
+            )
+        _native.check(status, "sa_pipeline_run_resident")
+        _merge_stats(stats, native_stats)
+        return out
+
     def _run_steps(
         self,
         q_cpu: torch.Tensor,

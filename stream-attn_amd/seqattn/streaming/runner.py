@@ -8,6 +8,9 @@ signatures and validation as the reference.  Additive options:
   allocates one and returns ``(out, lse)`` with the LSE copied to the host.
 * ``out`` may be a device tensor: the output then stays in HBM (finalized
   straight into ``out``) and no D2H is issued.
+* q, k and v may be device tensors on the plan's device (HBM-resident
+  inputs): the same Q super-block / K/V chunk schedule then reads them in
+  place, nothing crosses PCIe and the output is a device tensor.
 """
 
 from __future__ import annotations
@@ -20,7 +23,7 @@ import torch
 from ..config import StreamingAttentionConfig
 from ..planner import AttentionPlan
 from ..stats import StreamingAttentionStats
-from ..validation import require_pinned_inputs, validate_host_qkv
+from ..validation import require_pinned_inputs, validate_device_qkv, validate_host_qkv
 from .backend import resolve_backend
 from .executor import HipExecutorMixin
 from .workspace import CudaWorkspace
@@ -55,7 +58,12 @@ class StreamingAttentionRunner(HipExecutorMixin):
         cu_seqlens_q: torch.Tensor,
         cu_seqlens_k: torch.Tensor,
     ) -> tuple[list[int], list[int]]:
-        q_bounds, k_bounds = validate_host_qkv(q_cpu, k_cpu, v_cpu, cu_seqlens_q, cu_seqlens_k)
+        if q_cpu.device.type == "cuda":
+            q_bounds, k_bounds = validate_device_qkv(
+                q_cpu, k_cpu, v_cpu, cu_seqlens_q, cu_seqlens_k, self._device()
+            )
+        else:
+            q_bounds, k_bounds = validate_host_qkv(q_cpu, k_cpu, v_cpu, cu_seqlens_q, cu_seqlens_k)
         if q_cpu.shape[1:] != (self.plan.q_heads, self.plan.head_dim):
             raise ValueError("q shape does not match the runner plan")
         if k_cpu.shape[1:] != (self.plan.kv_heads, self.plan.head_dim):
@@ -65,6 +73,10 @@ class StreamingAttentionRunner(HipExecutorMixin):
         if q_cpu.shape[0] > self.plan.max_q_tokens or k_cpu.shape[0] > self.plan.max_kv_tokens:
             raise ValueError("input token count exceeds the runner plan")
         return q_bounds, k_bounds
+
+    def _device(self) -> torch.device:
+        device = self.plan.device
+        return device if device.index is not None else torch.device("cuda", torch.cuda.current_device())
 
     def _prepare_io(self, q_cpu, k_cpu, v_cpu, out: torch.Tensor) -> None:
         if self.config.require_pinned:
@@ -107,6 +119,10 @@ class StreamingAttentionRunner(HipExecutorMixin):
         if self.plan.output_mode == "device_consumer":
             raise ValueError("a device_consumer runner requires run_with_device_output()")
         scale = self.plan.head_dim**-0.5 if softmax_scale is None else float(softmax_scale)
+        if q_cpu.device.type == "cuda":
+            return self._call_resident(
+                q_cpu, k_cpu, v_cpu, q_bounds, k_bounds, scale, causal, out, stats, lse_out, return_lse
+            )
         if out is None:
             out = torch.empty(
                 q_cpu.shape, dtype=q_cpu.dtype, device="cpu",
@@ -125,6 +141,22 @@ class StreamingAttentionRunner(HipExecutorMixin):
         stats.wall_seconds += time.perf_counter() - started
         if return_lse:
             return result, lse.cpu() if lse_out is None else lse
+        return result
+
+    def _call_resident(self, q, k, v, q_bounds, k_bounds, scale, causal, out, stats, lse_out, return_lse):
+        if out is None:
+            out = torch.empty_like(q)
+        if out.shape != q.shape or out.dtype != q.dtype or out.device != q.device:
+            raise ValueError("out must be a device tensor matching q shape and dtype")
+        if out.stride(2) != 1 or any(t.stride(2) != 1 for t in (q, k, v)):
+            raise ValueError("device-resident tensors need unit stride over head_dim")
+        lse = self._lse_buffer(q.shape[0], lse_out, return_lse)
+        stats = self._prepare_stats(stats)
+        started = time.perf_counter()
+        result = self._run_resident(q, k, v, q_bounds, k_bounds, scale, causal, out, stats, lse)
+        stats.wall_seconds += time.perf_counter() - started
+        if return_lse:
+            return result, lse
         return result
 
     @torch.inference_mode()
@@ -150,6 +182,8 @@ class StreamingAttentionRunner(HipExecutorMixin):
         ``out[start:stop]``.  ``out`` may be a CPU tensor (D2H, as the
         reference) or a device tensor (the result stays in HBM).
         """
+        if q_cpu.device.type != "cpu":
+            raise ValueError("seqattn expects CPU-backed q, k, and v tensors")
         q_bounds, k_bounds = self._validate_inputs(q_cpu, k_cpu, v_cpu, cu_seqlens_q, cu_seqlens_k)
         if out.device.type not in {"cpu", "cuda"} or out.shape[0] != q_cpu.shape[0]:
             raise ValueError("out must be a CPU tensor with one row per query token")

@@ -26,6 +26,33 @@ def validate_host_qkv(
     """Check packed [tokens, heads, head_dim] CPU inputs; return segment bounds."""
     if any(t.device.type != "cpu" for t in (q, k, v)):
         raise ValueError("seqattn expects CPU-backed q, k, and v tensors")
+    return _validate_packed(q, k, v, cu_seqlens_q, cu_seqlens_k)
+
+
+def validate_device_qkv(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+    device: torch.device,
+) -> tuple[list[int], list[int]]:
+    """Check HBM-resident packed inputs (all on ``device``); return segment bounds.
+
+    Extension: the reference accepts CPU-backed inputs only (validation.py:13-14).
+    """
+    if any(t.device != device for t in (q, k, v)):
+        raise ValueError(f"device-resident q, k, and v must all live on {device}")
+    return _validate_packed(q, k, v, cu_seqlens_q, cu_seqlens_k)
+
+
+def _validate_packed(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    cu_seqlens_q: torch.Tensor,
+    cu_seqlens_k: torch.Tensor,
+) -> tuple[list[int], list[int]]:
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
         raise ValueError("q, k, and v must use packed [tokens, heads, head_dim] layout")
     if k.shape != v.shape:
@@ -58,4 +85,4 @@ def require_pinned_inputs(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor) -> 
         )
 
 
-__all__ = ["require_pinned_inputs", "validate_host_qkv"]
+__all__ = ["require_pinned_inputs", "validate_device_qkv", "validate_host_qkv"]

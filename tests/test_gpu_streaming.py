@@ -2,8 +2,15 @@
 
 Every case runs the product path (libseqattn_hip.so through the seqattn API
 or its kernel boundary) and compares with oracle/seqattn_oracle.py on the same
-seeded inputs.  Tolerances: bf16/fp16 output max-abs <= 2e-2 and natural-log
-LSE max-abs <= 1e-3 against the FP32-accumulated oracle.
+seeded inputs.  Tolerances against the FP32-accumulated oracle:
+
+* output max-abs <= 2e-2 and natural-log LSE max-abs <= 1e-3;
+* output relative L2 error <= 5e-3 (the bound of the reference's paged GPU
+  test, tests/test_paged_triton.py:87-88);
+* every element within 2^-5 * (|ref| + rms(ref)).  Long sequences have tiny
+  outputs (rms ~ sqrt(e / keys) for N(0,1) data), so the absolute bound alone
+  would accept a wrong result of the right magnitude; a correct kernel's
+  error is a few bf16 ulps of P and of the output (about 2^-9 relative).
 """
 
 from __future__ import annotations
@@ -20,6 +27,8 @@ pytestmark = pytest.mark.gpu
 
 O_TOL = 2e-2
 LSE_TOL = 1e-3
+REL_L2_TOL = 5e-3
+SCALED_TOL = 2.0**-5
 
 
 def announce(name: str) -> None:
@@ -45,12 +54,19 @@ def check(out, lse, ref_o, ref_l, rows=None):
         o, ref_o = o[rows], ref_o[rows]
         l, ref_l = l[:, rows], ref_l[:, rows]
     assert np.isfinite(o).all()
-    err_o = float(np.abs(o - ref_o).max())
+    diff = np.abs(o - ref_o)
+    err_o = float(diff.max())
+    ref_norm = float(np.sqrt(np.square(ref_o, dtype=np.float64).sum()))
+    rel_l2 = float(np.sqrt(np.square(diff, dtype=np.float64).sum())) / ref_norm if ref_norm > 0 else 0.0
+    rms = ref_norm / np.sqrt(ref_o.size) if ref_o.size else 0.0
+    scaled = float((diff / (np.abs(ref_o) + rms)).max()) if rms > 0 else 0.0
     finite = np.isfinite(ref_l)
     assert np.array_equal(np.isfinite(l), finite), "LSE -inf pattern differs"
     err_l = float(np.abs(l[finite] - ref_l[finite]).max()) if finite.any() else 0.0
-    print(f"    max|dO|={err_o:.3e} max|dLSE|={err_l:.3e}", flush=True)
+    print(f"    max|dO|={err_o:.3e} relL2={rel_l2:.3e} scaled={scaled:.3e} max|dLSE|={err_l:.3e}", flush=True)
     assert err_o <= O_TOL, err_o
+    assert rel_l2 <= REL_L2_TOL, rel_l2
+    assert scaled <= SCALED_TOL, scaled
     assert err_l <= LSE_TOL, err_l
 
 
@@ -152,6 +168,53 @@ def test_host_aliased_and_device_resident_outputs_are_bit_identical_to_host_mode
     check(results[0][0], results[0][1], ref_o, ref_l)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_device_resident_inputs_are_bit_identical_to_streamed(causal):
+    """HBM-resident Q/K/V run the same Q-block / K/V-chunk schedule in place:
+    output and LSE equal the pinned-host streamed run bit for bit."""
+    announce(f"device-resident inputs causal={causal}")
+    gen = torch.Generator().manual_seed(37)
+    q = pinned_randn((611, 8, 128), torch.bfloat16, gen)
+    k = pinned_randn((540, 2, 128), torch.bfloat16, gen)
+    v = pinned_randn((540, 2, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 200, 200, 611], dtype=torch.int32)
+    cu_k = torch.tensor([0, 150, 150, 540], dtype=torch.int32)
+    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=160, kv_chunk_tokens=96)
+    out, lse, runner = run(q, k, v, cu_q, cu_k, config, causal=causal)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out_d, lse_d = runner(qd, kd, vd, cu_q, cu_k, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert out_d.device.type == "cuda"
+    torch.testing.assert_close(out_d.cpu(), out, atol=0, rtol=0)
+    torch.testing.assert_close(lse_d.cpu(), lse, atol=0, rtol=0)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=160, kv_chunk=96, causal=causal)
+    check(out_d.cpu(), lse_d, ref_o, ref_l)
+
+
+def test_repeated_runs_are_bit_identical():
+    """Many workgroups per head and many K/V tiles per launch: three runs of
+    the same inputs must agree bit for bit (a race between the LDS DMA of one
+    wave and the reads of another shows up as run-to-run differences)."""
+    announce("determinism")
+    gen = torch.Generator().manual_seed(43)
+    q = pinned_randn((4096, 16, 128), torch.bfloat16, gen)
+    k = pinned_randn((6000, 16, 128), torch.bfloat16, gen)
+    v = pinned_randn((6000, 16, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 4096], dtype=torch.int32)
+    cu_k = torch.tensor([0, 6000], dtype=torch.int32)
+    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=4096, kv_chunk_tokens=3000)
+    out, lse, runner = run(q, k, v, cu_q, cu_k, config)
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    for _ in range(2):
+        again, lse_again = runner(qd, kd, vd, cu_q, cu_k, return_lse=True)
+        torch.cuda.synchronize()
+        torch.testing.assert_close(again.cpu(), out, atol=0, rtol=0)
+        torch.testing.assert_close(lse_again.cpu(), lse, atol=0, rtol=0)
+    rows = np.arange(0, 4096, 37)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=4096, kv_chunk=3000, causal=False, rows=rows)
+    check(out, lse, ref_o, ref_l, rows=rows)
+
+
 def test_runner_reuse_has_bounded_allocator_growth():
     announce("allocator growth")
     gen = torch.Generator().manual_seed(19)
@@ -204,11 +267,12 @@ def test_kernel_boundary_on_device_tensors_with_outliers():
     check(out.cpu(), lse, ref_o, ref_l)
 
 
-def test_config2_shape_streamed_1gib_sampled_rows():
-    """BASELINE config 2 shape: 65,536 tokens x 32 heads x 128, bf16, N(0,1)
-    seeded per 4,096-token chunk as the reference benchmark, streamed with a
-    1 GiB workspace and 4,096-token K/V chunks; sampled rows vs the oracle."""
-    announce("config2 streamed 1GiB")
+def test_65k_tokens_32_heads_streamed_1gib_and_resident():
+    """65,536 tokens x 32 heads x 128, bf16, N(0,1) seeded per 4,096-token
+    chunk as the reference benchmark: streamed with a 1 GiB workspace and
+    4,096-token K/V chunks (sampled rows vs the oracle), then fully resident
+    in HBM (bit-identical to the streamed run)."""
+    announce("65k x 32h streamed 1GiB")
     from oracle.seqattn_oracle import seeded_normal_chunks
 
     n, heads, d = 65536, 32, 128
@@ -221,3 +285,10 @@ def test_config2_shape_streamed_1gib_sampled_rows():
     ref_o, ref_l = oracle(q, k, v, [0, n], [0, n], q_chunk=runner.plan.q_chunk_tokens, kv_chunk=4096,
                           causal=False, rows=rows)
     check(out, lse, ref_o, ref_l, rows=rows)
+
+    announce("65k x 32h fully resident in HBM")
+    qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
+    out_d, lse_d = runner(qd, kd, vd, cu, cu, return_lse=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out_d.cpu(), out, atol=0, rtol=0)
+    torch.testing.assert_close(lse_d.cpu(), lse, atol=0, rtol=0)

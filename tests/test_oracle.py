@@ -148,6 +148,64 @@ def test_oracle_catches_planted_mistakes():
     assert np.abs(buggy - ref_o).max() > 1e-2
 
 
+class _NumpyWith:
+    """numpy with some functions replaced (plants a mistake in the oracle)."""
+
+    def __init__(self, **overrides):
+        self._overrides = overrides
+
+    def __getattr__(self, name):
+        return self._overrides.get(name, getattr(np, name))
+
+
+def _shifted_attend(delta_shift=0, delta_pos=0):
+    import oracle.seqattn_oracle as mod
+
+    original = mod._attend_heads
+
+    def attend(q_tile, k, v, kv_range, group, k_start, k_stop, kv_chunk, scale, causal, q_pos, shift):
+        return original(q_tile, k, v, kv_range, group, k_start, k_stop, kv_chunk, scale, causal,
+                        q_pos + delta_pos, shift + delta_shift)
+
+    return attend
+
+
+MUTANTS = {
+    # GQA: query head h must read K/V head h // group, not h % kv_heads.
+    "gqa_head_map": ("np", _NumpyWith(repeat=lambda a, r, axis: np.tile(a, (1, r, 1)))),
+    # base-2 exponent where the reference's FP32 path uses natural exp
+    "exp_base": ("np", _NumpyWith(exp=lambda x, out=None: np.exp2(x, out=out))),
+    # bottom-right causal alignment dropped (shift Lk - Lq treated as 0)
+    "causal_shift": ("_attend_heads", _shifted_attend(delta_shift=-3)),
+    # query positions off by one
+    "query_position": ("_attend_heads", _shifted_attend(delta_pos=1)),
+}
+
+
+@pytest.mark.parametrize("mutant", sorted(MUTANTS))
+def test_dense_pin_catches_mistakes_planted_in_the_oracle(mutant, monkeypatch):
+    """Each plausible mistake, planted in the oracle itself, fails the dense
+    float64 closed form on a causal GQA case where it matters."""
+    import oracle.seqattn_oracle as mod
+
+    rng = np.random.default_rng(23)
+    q = rng.standard_normal((14, 4, 16)).astype(np.float32)
+    k = rng.standard_normal((17, 2, 16)).astype(np.float32)
+    v = rng.standard_normal((17, 2, 16)).astype(np.float32)
+    cu_q, cu_k = [0, 14], [0, 17]
+    ref_o, ref_l = dense_attention_f64(q, k, v, cu_q, cu_k, causal=True)
+    good_o, good_l = chunked_attention(q, k, v, cu_q, cu_k, q_chunk_tokens=5, kv_chunk_tokens=4, causal=True)
+    assert np.abs(good_o - ref_o).max() < 1e-5
+    name, replacement = MUTANTS[mutant]
+    monkeypatch.setattr(mod, name, replacement)
+    bad_o, bad_l = chunked_attention(q, k, v, cu_q, cu_k, q_chunk_tokens=5, kv_chunk_tokens=4, causal=True)
+    finite = np.isfinite(ref_l) & np.isfinite(bad_l)
+    worst = max(float(np.nan_to_num(np.abs(bad_o - ref_o), nan=1.0).max()),
+                float(np.abs(bad_l[finite] - ref_l[finite]).max()) if finite.any() else 0.0,
+                float((np.isfinite(ref_l) != np.isfinite(bad_l)).any()))
+    assert worst > 1e-3, mutant
+
+
 def test_seeded_inputs_follow_torch_generator_stream():
     a = seeded_normal_chunks(10_000, 2, 8, seed=0, tensor_index=1, chunk_tokens=4096, dtype=torch.float32)
     g = torch.Generator(device="cpu").manual_seed(0 + 1 * 1_000_003 + 2)
@@ -155,8 +213,8 @@ def test_seeded_inputs_follow_torch_generator_stream():
     assert torch.equal(a[8192:], expected_tail)
 
 
-def test_config1_cpu_plumbing_shape():
-    """fp32 [4096, 8, 64], seed 0, q block 1024, kv chunk 512 vs dense fp64."""
+def test_cpu_plumbing_4096_tokens_8_heads():
+    """CPU plumbing workload: fp32 [4096, 8, 64], seed 0, q block 1024, kv chunk 512 vs dense fp64."""
     g = torch.Generator().manual_seed(0)
     q = torch.randn((4096, 8, 64), generator=g).numpy()
     k = torch.randn((4096, 8, 64), generator=g).numpy()
