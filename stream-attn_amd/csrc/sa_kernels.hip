@@ -33,9 +33,11 @@
 //   key assignment is the same on both sides: key = 16c + 8(e/4) + 4h + e%4.
 //   Each K/V fragment read from LDS feeds QB MFMAs.
 //
-// Online softmax with a thresholded rescale: the running maximum m only moves
-// (and acc, l are rescaled by exp2(m_old - m_new)) when some logit of the wave
-// exceeds m + 8; otherwise p = exp2(s*scale - m) <= 2^8 against the kept m.
+// Online softmax with a thresholded rescale: a query's running maximum m only
+// moves (and its acc, l are rescaled by exp2(m_old - m_new)) when one of its
+// logits exceeds m + 8; otherwise p = exp2(s*scale - m) <= 2^8 against the
+// kept m.  The decision is per query, so results do not depend on how queries
+// are grouped into wavefronts or Q blocks.
 // (m, l, acc) remains an exact representation of the partial softmax:
 // out = acc / l and LSE = m + log2(l) are unchanged, and P keeps bf16's
 // relative precision.  The row sum l is accumulated per lane half and the two
@@ -334,11 +336,14 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
         grow = grow || (mx[qb] > m_run[qb] + kRescaleThreshold);
       }
       // Rescale only when some logit of the wave left the [.., m + 8] window.
+      // Inside the branch each query still decides for itself (both lane
+      // halves of a query see the same decision), so a query's result never
+      // depends on which other queries share its wavefront.
       if (__ballot(grow) != 0) {
 #pragma unroll
         for (int qb = 0; qb < QB; ++qb) {
           const float full = fmaxf(mx[qb], __shfl_xor(mx[qb], 32));
-          const float m_new = fmaxf(m_run[qb], full);
+          const float m_new = full > m_run[qb] + kRescaleThreshold ? full : m_run[qb];
           const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
           l_part[qb] *= alpha;
 #pragma unroll

@@ -4,23 +4,55 @@ Drop-in for the reference package's tensor-mode and device-consumer API
 (reference src/seqattn_core/__init__.py:1-77).  Q/K/V stay in caller-owned
 (pinned) host DRAM; a resident Q super-block and a K/V ring live in a bounded
 HBM workspace; the chunk-update / finalize kernels and the copy pipeline are
-native gfx950 code in ``_lib/libseqattn_hip.so``.
+native gfx950 code in ``_lib/libseqattn_hip.so``.  Paged mode
+(``PagedAttentionRunner`` over memory or aligned on-disk page stores) runs on
+the same kernels and pipeline.
 """
 
 from .api import StreamingAttentionRunner, streaming_attn_func, streaming_attn_varlen_func
 from .config import PagedAttentionConfig, StreamingAttentionConfig
+from .paged import (
+    CallbackOutputSink,
+    HostMemoryPlan,
+    HostMemorySnapshot,
+    KVLayout,
+    MemoryPageSink,
+    MemoryPageSource,
+    PagedAttentionRunner,
+    PageDescriptor,
+    PageSink,
+    PageSource,
+    TensorLayout,
+)
 from .planner import AttentionPlan, build_plan
 from .stats import PagedAttentionStats, ProjectedAttentionStats, StreamingAttentionStats
+from .storage import NvmeOutputSink, NvmeQKVStore, NvmeQKVWriter, ephemeral_nvme_directory, load_nvme_output
 
 __all__ = [
     "AttentionPlan",
+    "CallbackOutputSink",
+    "HostMemoryPlan",
+    "HostMemorySnapshot",
+    "KVLayout",
+    "MemoryPageSink",
+    "MemoryPageSource",
+    "NvmeOutputSink",
+    "NvmeQKVStore",
+    "NvmeQKVWriter",
+    "PageDescriptor",
+    "PageSink",
+    "PageSource",
     "PagedAttentionConfig",
+    "PagedAttentionRunner",
     "PagedAttentionStats",
     "ProjectedAttentionStats",
     "StreamingAttentionConfig",
     "StreamingAttentionRunner",
     "StreamingAttentionStats",
+    "TensorLayout",
     "build_plan",
+    "ephemeral_nvme_directory",
+    "load_nvme_output",
     "streaming_attn_func",
     "streaming_attn_varlen_func",
 ]
