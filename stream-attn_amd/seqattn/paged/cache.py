@@ -9,7 +9,7 @@ host memory.
 Different storage: each slot holds a page's K/V record image (K rows at 0, V
 rows at the record's ``v_offset``, INT8 scales after them) in page-locked
 memory, so a hit is served by the copy engine straight from the slot and a
-miss from an aligned store is read into its slot with one O_DIRECT read (the
+miss from an aligned store is read into its slot as one whole record (the
 reference copies between an mmap region and a staging tensor on every hit and
 insert).  Slots referenced by copies still in flight are never evicted.
 """

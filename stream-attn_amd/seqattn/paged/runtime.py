@@ -13,9 +13,9 @@ Same entry point, arguments, validation and stats as the reference's
   multiples of the chunk within the segment as in tensor mode;
 * page data reaches the copy engines from page-locked memory with no host
   copy where possible: the DRAM cache's slots are page-locked (hits are copied
-  straight from the slot), misses from an aligned store are read with one
-  O_DIRECT read into a cache slot or a staging slot, and page-locked caller
-  tensors of a ``MemoryPageSource`` are read in place;
+  straight from the slot), misses from an aligned store are read as whole
+  records into a cache slot or a staging slot, and page-locked caller tensors
+  of a ``MemoryPageSource`` are read in place;
 * K/V pages that the bottom-right causal mask hides from a whole Q block are
   neither read nor copied;
 * ``run_with_device_output`` keeps the output in HBM (device-consumer mode,
@@ -331,41 +331,47 @@ class PagedAttentionRunner:
         kernel_start = torch.cuda.Event(enable_timing=True)
         kernel_end = torch.cuda.Event(enable_timing=True)
         kernel_start.record(compute)
+        # Every Q block in execution order, so the next block's query pages can
+        # be read while the current block streams its K/V.
+        blocks = []
         group_index = 0
-
-        for segment, (q_pages, kv_pages) in enumerate(zip(q_pages_by_segment, kv_pages_by_segment)):
-            q0, q1 = q_bounds[segment], q_bounds[segment + 1]
-            k0, k1 = k_bounds[segment], k_bounds[segment + 1]
-            if q1 == q0:
+        for segment, q_pages in enumerate(q_pages_by_segment):
+            if q_bounds[segment + 1] == q_bounds[segment]:
                 continue
-            shift = (k1 - k0) - (q1 - q0)
             for group in plan_q_groups(q_pages, state.q_rows):
-                out_slot = group_index % max(1, len(state.out_stage))
+                for position, block in enumerate(group.blocks):
+                    blocks.append((segment, group, group_index, block, position == len(group.blocks) - 1))
                 group_index += 1
-                if state.out_stage:
-                    state.wait_out_slot(out_slot, self, stats)
-                for block in group.blocks:
-                    n = block.rows
-                    global_start = q0 + block.segment_start
-                    # Q block -> resident Q buffer.
-                    with self._range("seqattn_paged:q_h2d"):
-                        q_address = state.load_q_rows(self, block, q_row_bytes, stats, global_start)
-                        _native.check(lib.sa_pipeline_load_q(handle, q_address, n, compute_ptr, native_ref),
-                                      "sa_pipeline_load_q")
-                        state.q_loaded()
-                    stats.q_chunks += 1
-                    stats.kv_page_scans += 1
-                    # K/V pages -> gathered ring chunks -> update launches.
-                    with self._range("seqattn_paged:kv_scan"):
-                        self._scan(state, lib, handle, compute_ptr, native_ref, plan, kv_pages, k0, n,
-                                   block.segment_start, shift, scale, causal, depth, kv_row_bytes, stats)
-                    # Finalize and deliver the block's output.
-                    with self._range("seqattn_paged:finalize"):
-                        self._deliver(state, lib, handle, compute, compute_ptr, native_ref, block, group,
-                                      out_slot, n, global_start, q_row_bytes, device_out, transform, lse_ptr,
-                                      lse_stride, stats)
-                if state.out_stage:
-                    state.write_group(self, group, out_slot, stats)
+
+        for index, (segment, group, group_id, block, group_end) in enumerate(blocks):
+            q0 = q_bounds[segment]
+            k0, k1 = k_bounds[segment], k_bounds[segment + 1]
+            shift = (k1 - k0) - (q_bounds[segment + 1] - q0)
+            out_slot = group_id % max(1, len(state.out_stage))
+            if state.out_stage and block.group_offset == 0:
+                state.wait_out_slot(out_slot, self, stats)
+            n = block.rows
+            global_start = q0 + block.segment_start
+            # Q block -> resident Q buffer.
+            with self._range("seqattn_paged:q_h2d"):
+                q_address = state.load_q_rows(self, block, q_row_bytes, stats, global_start)
+                _native.check(lib.sa_pipeline_load_q(handle, q_address, n, compute_ptr, native_ref),
+                              "sa_pipeline_load_q")
+                state.q_loaded()
+            stats.q_chunks += 1
+            stats.kv_page_scans += 1
+            following = blocks[index + 1][3] if index + 1 < len(blocks) else None
+            prefetch = (lambda b=following: state.prefetch_q(b)) if following is not None else None
+            # K/V pages -> gathered ring chunks -> update launches.
+            with self._range("seqattn_paged:kv_scan"):
+                self._scan(state, lib, handle, compute_ptr, native_ref, plan, kv_pages_by_segment[segment], k0,
+                           n, block.segment_start, shift, scale, causal, depth, kv_row_bytes, stats, prefetch)
+            # Finalize and deliver the block's output.
+            with self._range("seqattn_paged:finalize"):
+                self._deliver(state, lib, handle, compute, compute_ptr, native_ref, block, group, out_slot, n,
+                              global_start, q_row_bytes, device_out, transform, lse_ptr, lse_stride, stats)
+            if state.out_stage and group_end:
+                state.write_group(self, group, out_slot, stats)
         kernel_end.record(compute)
         kernel_end.synchronize()
         stats.gpu_kernel_seconds += kernel_start.elapsed_time(kernel_end) / 1e3
@@ -375,7 +381,7 @@ class PagedAttentionRunner:
         stats.state_spills += native.kv_tiles
 
     def _scan(self, state, lib, handle, compute_ptr, native_ref, plan, kv_pages, k0, q_tokens, q_local_offset,
-              shift, scale, causal, depth, kv_row_bytes, stats):
+              shift, scale, causal, depth, kv_row_bytes, stats, prefetch=None):
         """Stream one segment's K/V pages through the ring for one Q block."""
         if causal:
             visible_end = q_local_offset + q_tokens + shift
@@ -412,6 +418,8 @@ class PagedAttentionRunner:
         for _ in range(min(depth, len(pages))):
             loads.append(state.submit_kv(self, pages[position], k0, issue, queue, stats))
             position += 1
+        if prefetch is not None:
+            prefetch()
         while loads:
             load = loads.popleft()
             if load.future is not None:
@@ -491,6 +499,8 @@ class _RunState:
         self.pinned_registered = 0
         self.memory_plan = None
         self.q_event = None
+        self.q_event_pending = False
+        self.q_reads = None
         self.device_slot = 0
         self.kv_is_nvme = False
         self.q_is_nvme = False
@@ -620,7 +630,7 @@ class _RunState:
         destination = slab.bytes(slot)
         reader = self.kv_reader
         if hasattr(reader, "read_kv_record"):
-            return reader.read_kv_record(page, memoryview(destination.numpy()))
+            return reader.read_kv_record(page, destination)
         layout = self.cache.layout
         dtype = layout.storage_torch_dtype
         shape = (record.padded_tokens, layout.heads, layout.head_dim)
@@ -639,16 +649,31 @@ class _RunState:
 
     # --- Q rows --------------------------------------------------------------
 
-    def load_q_rows(self, runner, block, q_row_bytes, stats, global_start) -> int:
-        stats.q_pages += sum(1 for piece in block.pieces if piece.page_offset == 0)
+    def prefetch_q(self, block) -> None:
+        """Start reading the next block's query pages into the Q staging
+        buffer once the current block's Q copy has left it."""
         if self.zero_copy_q is not None:
-            return self.zero_copy_q.pinned_q_rows(global_start, global_start + block.rows).data_ptr()
+            return
+        self._submit_q_reads(block)
+
+    def _submit_q_reads(self, block) -> None:
         if self.q_event_pending:
             self.q_event.synchronize()
+            self.q_event_pending = False
         futures = []
         for piece in block.pieces:
             target = self.q_stage[piece.block_offset : piece.block_offset + piece.rows]
             futures.append(self.pool.submit(self._read_q_piece, piece, target))
+        self.q_reads = (block, futures)
+
+    def load_q_rows(self, runner, block, q_row_bytes, stats, global_start) -> int:
+        stats.q_pages += sum(1 for piece in block.pieces if piece.page_offset == 0)
+        if self.zero_copy_q is not None:
+            return self.zero_copy_q.pinned_q_rows(global_start, global_start + block.rows).data_ptr()
+        if self.q_reads is None or self.q_reads[0] is not block:
+            self._submit_q_reads(block)
+        futures = self.q_reads[1]
+        self.q_reads = None
         wait_started = time.perf_counter()
         for future in futures:
             runner._account_read(stats, future.result(), self.q_is_nvme)

@@ -1,8 +1,9 @@
 """Page-locked host slabs carved into 4,096-byte aligned record slots.
 
 One allocation per slab (``torch.empty(..., pin_memory=True)``, i.e.
-hipHostMalloc), so the copy engines read every slot directly and O_DIRECT
-reads land in it without a bounce copy.  Each slot tracks the H2D copies
+hipHostMalloc), so the copy engines read every slot directly.  (O_DIRECT
+cannot target this memory: the kernel refuses to map it for a direct
+transfer, so direct-I/O reads go through an aligned bounce buffer.)  Each slot tracks the H2D copies
 still reading it: ``hold`` counts fragments that reference the slot and are
 not yet copied, ``release`` attaches the event that marks their copy done,
 and ``wait_reusable`` blocks until no copy can still read the slot.

@@ -4,9 +4,8 @@ validation rules, so stores written by either implementation load here).
 
 Besides the protocol's ``read_q`` / ``read_kv`` (through aligned bounce
 buffers registered as ``bounce`` host memory), the reader offers
-``read_kv_record``: one O_DIRECT read of a whole K/V record straight into a
-caller buffer, used by the paged runtime to fill its page-locked slots with no
-intermediate copy.
+``read_kv_record``: one read of a whole K/V record into a caller buffer (the
+paged runtime's page-locked slots), with no per-tensor unpacking.
 """
 
 from __future__ import annotations
@@ -112,21 +111,33 @@ class _NvmePageReader(PageReader):
             self.free.put(buffer)
         return PageReadMetrics(read_seconds=elapsed, logical_bytes=logical, physical_bytes=page.storage_bytes)
 
-    def read_kv_record(self, page: PageDescriptor, destination: memoryview) -> PageReadMetrics:
-        """Read the whole K/V record of ``page`` into ``destination`` (at least
-        ``page.storage_bytes`` long; 4,096-byte aligned for O_DIRECT)."""
-        started = time.perf_counter()
-        view = destination[: page.storage_bytes]
-        try:
-            pread_exact(self.kv_fd, view, page.file_offset, self.direct_io, self.store.kv_path)
-        finally:
-            view.release()
+    def read_kv_record(self, page: PageDescriptor, destination: torch.Tensor) -> PageReadMetrics:
+        """Read the whole K/V record of ``page`` into the uint8 CPU tensor
+        ``destination`` (at least ``page.storage_bytes`` long).
+
+        Buffered stores read straight into it.  O_DIRECT stores read into an
+        aligned bounce buffer and copy: the kernel cannot map GPU-registered
+        page-locked memory for a direct transfer (the read fails with EFAULT).
+        """
+        if self.direct_io:
+            buffer, elapsed = self._read_record(self.kv_fd, self.store.kv_path, page)
+            try:
+                destination[: page.storage_bytes].copy_(buffer.bytes[: page.storage_bytes])
+            finally:
+                self.free.put(buffer)
+        else:
+            started = time.perf_counter()
+            view = memoryview(destination.numpy())[: page.storage_bytes]
+            try:
+                pread_exact(self.kv_fd, view, page.file_offset, False, self.store.kv_path)
+            finally:
+                view.release()
+            elapsed = time.perf_counter() - started
         logical = 2 * page.valid_tokens * self.store.kv_layout.storage_bytes_per_token
         if self.store.kv_layout.storage_dtype == "int8":
             groups = math.ceil(page.valid_tokens / self.store.kv_layout.quant_group_tokens)
             logical += 2 * groups * self.store.kv_layout.heads * 2
-        return PageReadMetrics(read_seconds=time.perf_counter() - started, logical_bytes=logical,
-                               physical_bytes=page.storage_bytes)
+        return PageReadMetrics(read_seconds=elapsed, logical_bytes=logical, physical_bytes=page.storage_bytes)
 
     def close(self) -> None:
         if self.closed:

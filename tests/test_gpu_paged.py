@@ -141,16 +141,20 @@ def test_memory_source_pinned_zero_copy_and_staged_paths_agree(pinned):
     oracle_check(out, q, k, v, cu_q, cu_k, q_chunk=384, kv_chunk=256, causal=True, rows=rows)
 
 
-def test_nvme_store_with_rolling_cache_and_staging(tmp_path):
-    announce("nvme store, cache smaller than K/V")
+@pytest.mark.parametrize("direct_io", [False, True])
+def test_nvme_store_with_rolling_cache_and_staging(tmp_path, direct_io):
+    announce(f"nvme store, cache smaller than K/V, direct_io={direct_io}")
     q, k, v = _inputs(2048, 2048, 4, 4, 128, 11, outliers=True)
     cu = bounds([2048])
     page_bytes = 128 * 4 * 128 * 2  # 128-token pages, 256 KiB K+V records
-    store = NvmeQKVWriter.from_tensors(tmp_path / "store", q, k, v, cu, cu, page_target_bytes=page_bytes,
-                                       block_n=64, kv_storage_dtype="bf16", direct_io=False)
+    try:
+        store = NvmeQKVWriter.from_tensors(tmp_path / "store", q, k, v, cu, cu, page_target_bytes=page_bytes,
+                                           block_n=64, kv_storage_dtype="bf16", direct_io=direct_io)
+    except RuntimeError as error:
+        pytest.skip(f"no O_DIRECT support here: {error}")
     # 16 K/V pages; cache of 6 record slots (4 hot + 2 rolling); 4 Q blocks re-scan K/V.
     config = paged_config(q_chunk=512, kv_chunk=512, page_target_bytes=page_bytes, cache_mib=1, pinned_mib=8,
-                          depth=3)
+                          depth=3, direct_io=direct_io)
     config = replace(config, host_memory_budget_bytes=6 * 256 * 1024 + 13 * 2**20, cache_hot_fraction=0.7)
     out = torch.empty_like(q)
     stats = PagedAttentionStats()

@@ -325,7 +325,7 @@ def test_store_round_trip_buffered(tmp_path):
             assert torch.equal(ko[: page.valid_tokens], k[page.token_start : page.token_stop])
             assert torch.equal(vo[: page.valid_tokens], v[page.token_start : page.token_stop])
             raw = torch.empty(page.storage_bytes, dtype=torch.uint8)
-            reader.read_kv_record(page, memoryview(raw.numpy()))
+            reader.read_kv_record(page, raw)
             k_rec = raw[: page.k_bytes].view(torch.float32).view(page.padded_tokens, 2, 16)
             v_rec = raw[page.v_offset : page.v_offset + page.v_bytes].view(torch.float32).view(page.padded_tokens, 2, 16)
             assert torch.equal(k_rec[: page.valid_tokens], k[page.token_start : page.token_stop])
