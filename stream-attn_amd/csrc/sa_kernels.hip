@@ -9,11 +9,14 @@
 // also writes LSE = (m + log2 l) * ln 2, which the reference does not produce.
 //
 // Update kernel work decomposition:
-//   workgroup = 4 wavefronts, one per SIMD; wave w owns QB blocks of 32
-//   queries (QB = 2 for head_dim <= 128, else 1) of one query head, so a
-//   workgroup covers 128 * QB queries.  Workgroups are numbered head-major and
-//   dealt to the 8 XCDs in contiguous runs, so the workgroups resident on one
-//   XCD share one head's K/V stream in that XCD's L2.
+//   head_dim 128: workgroup = 8 wavefronts (two per SIMD), each owning 32
+//   queries of one query head (256 queries per workgroup); while one wave of
+//   a SIMD waits on LDS or on the MFMA pipe the other issues.  Other head
+//   dims: 4 wavefronts (one per SIMD) owning QB blocks of 32 queries (QB = 2
+//   for head_dim <= 64, 1 for 256), so each K/V fragment read from LDS feeds
+//   QB MFMAs.  Workgroups are numbered head-major and dealt to the 8 XCDs in
+//   contiguous runs, so the workgroups resident on one XCD share one head's
+//   K/V stream in that XCD's L2.
 //   K/V stream through LDS in 64-key tiles, two stages: the tile after the one
 //   being computed is fetched by global_load_lds_dwordx4 (HBM/L2 -> LDS with
 //   no register staging) while the MFMAs run; one barrier per tile.
@@ -65,9 +68,6 @@ typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 #define SA_LDS __attribute__((address_space(3)))
 #define SA_GLOBAL __attribute__((address_space(1)))
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
-constexpr int kTileKeys = 64;  // keys per LDS stage
 constexpr int kSubKeys = 32;   // keys per softmax step
 constexpr float kRescaleThreshold = 8.0f;  // log2 units
 
@@ -112,15 +112,37 @@ struct UpdateParams {
 // Row r (0..15) of a 32x32 C tile held in register i of a lane in half h.
 __device__ inline int c_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
 
+// Positive factor applied to raw logits inside the exponent's FMA (so the
+// running max can be taken before scaling): |scale|, at least 1e-30.
+__device__ inline float scale_factor(float scale_log2) { return fmaxf(fabsf(scale_log2), 1e-30f); }
+
+// Sign-bit mask that negates every 16-bit element of a Q fragment when the
+// scale is negative: s * scale == (-q . k) * |scale|, exactly.
+__device__ inline u32x4 q_sign(float scale_log2) {
+  const uint32_t m = scale_log2 < 0.f ? 0x80008000u : 0u;
+  return u32x4{m, m, m, m};
+}
+
 template <int DP>
 struct Geometry {
   static constexpr int G = DP / 8;             // 16-byte granules per K/V row
   static constexpr int ROW_BYTES = DP * 2;
-  static constexpr int QB = DP <= 128 ? 2 : 1;  // 32-query blocks per wave
-  static constexpr int BLOCK_M = kWaves * 32 * QB;
-  static constexpr int TILE_BYTES = kTileKeys * ROW_BYTES;  // K (or V) part of a stage
+  // head_dim 128: eight wavefronts (two per SIMD) of 32 queries; the second
+  // wave on a SIMD issues while the first waits on LDS or the MFMA pipe.
+  // Otherwise four wavefronts of 64 queries (32 for head_dim 256), each K/V
+  // fragment read from LDS feeding two MFMAs.
+  static constexpr int WAVES = DP == 128 ? 8 : 4;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int QB = DP >= 128 ? 1 : 2;  // 32-query blocks per wave
+  static constexpr int BLOCK_M = WAVES * 32 * QB;
+  static constexpr int TILE_KEYS = 64;                       // keys per LDS stage
+  static constexpr int TILE_BYTES = TILE_KEYS * ROW_BYTES;  // K (or V) part of a stage
   static constexpr int ROWS_PER_DMA = 1024 / ROW_BYTES;     // rows per wave-wide 1 KB DMA
-  static constexpr int DMA_PER_WAVE = kTileKeys / ROWS_PER_DMA / kWaves;
+  static constexpr int DMA_PER_WAVE = TILE_KEYS / ROWS_PER_DMA / WAVES;
+  // K fragments requested ahead of their MFMAs, and V^T d-blocks per batch
+  // of transposing reads (bounded by the 256 VGPRs of an eight-wave kernel).
+  static constexpr int KB = DP == 128 ? 2 : DP / 16;
+  static constexpr int VB = DP == 128 ? 2 : (DP / 32 < 4 ? DP / 32 : 4);
   static_assert(DMA_PER_WAVE >= 1, "tile too small for the workgroup");
   // Granule swizzle: rows r..r+7 (r % 8 == 0) get 8 distinct XOR masks and
   // rows r..r+3 (r % 4 == 0) masks that differ in bits 1-2.
@@ -131,7 +153,7 @@ struct Geometry {
 };
 
 template <typename Op, int DP, bool CAUSAL, bool INIT>
-__global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) {
+__global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const UpdateParams p) {
   using Geo = Geometry<DP>;
   constexpr int QB = Geo::QB;
   constexpr int QC = DP / 16;  // 16-wide d slices of the QK^T contraction
@@ -176,7 +198,7 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
     for (int c = 0; c < QC; ++c) {
       const int d = 16 * c + 8 * hf;
       if (ok && d < p.head_dim)
-        qf[qb][c] = *reinterpret_cast<const u32x4*>(qp + (int64_t)qi[qb] * p.sq_t + d);
+        qf[qb][c] = *reinterpret_cast<const u32x4*>(qp + (int64_t)qi[qb] * p.sq_t + d) ^ q_sign(p.scale_log2);
       else
         qf[qb][c] = u32x4{0, 0, 0, 0};
     }
@@ -220,13 +242,13 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
     const int lim = p.q_local_offset + q_last + p.causal_shift - p.kv_local_offset + 1;
     kv_end = max(0, min(kv_end, lim));
   }
-  const int ntiles = (kv_end + kTileKeys - 1) / kTileKeys;
+  const int ntiles = (kv_end + Geo::TILE_KEYS - 1) / Geo::TILE_KEYS;
 
-  // Scale handling: for a positive scale the max is taken on raw logits and
-  // the scale is fused into the exponent's FMA; otherwise logits are scaled
-  // first (the max of s * c for c <= 0 is not c * max(s)).
-  const bool scale_pos = p.scale_log2 > 0.f;
-  const float cf = scale_pos ? p.scale_log2 : 1.f;
+  // The scale is fused into the exponent's FMA and the max is taken on raw
+  // logits, which needs a positive factor: a negative scale was folded into
+  // the sign of Q when the fragments were loaded, and a zero scale becomes
+  // 1e-30 (every logit then rounds to the same exponent, as with zero).
+  const float cf = scale_factor(p.scale_log2);
 
   // HBM/L2 -> LDS DMA of key tile [kt, kt + 64) into stage st.  Each lane's
   // element offset within a tile is fixed (precomputed below); the tile base
@@ -250,7 +272,7 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
     uint8_t* v_stage = stage + Geo::TILE_BYTES;
     const uint16_t* kt_base = kp + (int64_t)kt * p.sk_t;
     const uint16_t* vt_base = vp + (int64_t)kt * p.sv_t;
-    const bool tail = kt + kTileKeys > p.kv_tokens;
+    const bool tail = kt + Geo::TILE_KEYS > p.kv_tokens;
 #pragma unroll
     for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
       const int chunk = wave * Geo::DMA_PER_WAVE + i;
@@ -269,7 +291,7 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
 
   // Tile t is computed from `cur` while tile t+1 streams into `next`.
   auto tile = [&](int t, const uint8_t* cur, uint8_t* next) {
-    const int kt = t * kTileKeys;
+    const int kt = t * Geo::TILE_KEYS;
     // Every wave waits for its own DMA of tile t before the barrier, so after
     // it all 64 rows of `cur` are in LDS.  LDS DMA is counted by vmcnt, which
     // a workgroup-scope fence does not wait for: without this explicit wait a
@@ -277,35 +299,35 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
     // barrier also guarantees `next` (tile t-1) is no longer being read.
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
-    if (t + 1 < ntiles) issue_tile(kt + kTileKeys, next);
+    if (t + 1 < ntiles) issue_tile(kt + Geo::TILE_KEYS, next);
     const uint8_t* k_stage = cur;
     const uint8_t* v_stage = cur + Geo::TILE_BYTES;
 
 #pragma unroll
-    for (int sub = 0; sub < kTileKeys / kSubKeys; ++sub) {
+    for (int sub = 0; sub < Geo::TILE_KEYS / kSubKeys; ++sub) {
       const int rb = sub * kSubKeys;  // tile-relative first key of this step
       const int key0 = kt + rb;
 
       // S^T for the 32 keys x (32 * QB) queries of this wave.  All K
       // fragments of the step are requested before the first MFMA so the
       // LDS latency is paid once.
-      u32x4 kf[QC];
-#pragma unroll
-      for (int c = 0; c < QC; ++c)
-        kf[c] = *reinterpret_cast<const u32x4*>(k_stage + Geo::offset(rb + lr, 2 * c + hf));
       f32x16 s[QB];
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) s[qb] = f32x16{};
+      constexpr int KB = Geo::KB;
 #pragma unroll
-      for (int c = 0; c < QC; ++c) {
+      for (int c0 = 0; c0 < QC; c0 += KB) {
+        u32x4 kf[KB];
 #pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[qb] = Op::mma(kf[c], qf[qb][c], s[qb]);
+        for (int c = 0; c < KB; ++c)
+          kf[c] = *reinterpret_cast<const u32x4*>(k_stage + Geo::offset(rb + lr, 2 * (c0 + c) + hf));
+#pragma unroll
+        for (int c = 0; c < KB; ++c) {
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) s[qb] = Op::mma(kf[c], qf[qb][c0 + c], s[qb]);
+        }
       }
 
-      if (!scale_pos) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) s[qb] *= p.scale_log2;
-      }
       bool need_mask = key0 + kSubKeys > p.kv_tokens;
       if (CAUSAL)
         need_mask = need_mask || (p.kv_local_offset + key0 + kSubKeys - 1 >
@@ -381,7 +403,7 @@ __global__ __launch_bounds__(kThreads) void update_kernel(const UpdateParams p) 
       const int grp = lane >> 4;
       const int gi = lane & 15;
       const uint32_t v_lds = (uint32_t)(uintptr_t)(const SA_LDS uint8_t*)(v_stage);
-      constexpr int VB = DB < 4 ? DB : 4;
+      constexpr int VB = Geo::VB;
 #pragma unroll
       for (int d0 = 0; d0 < DB; d0 += VB) {
         u32x4 vf[VB][2];
@@ -500,14 +522,14 @@ hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t 
   const dim3 grid((unsigned)(8 * (int64_t)p.xcd_run));
   if (causal) {
     if (init)
-      hipLaunchKernelGGL((update_kernel<Op, DP, true, true>), grid, dim3(kThreads), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, true, true>), grid, dim3(Geo::THREADS), 0, s, p);
     else
-      hipLaunchKernelGGL((update_kernel<Op, DP, true, false>), grid, dim3(kThreads), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, true, false>), grid, dim3(Geo::THREADS), 0, s, p);
   } else {
     if (init)
-      hipLaunchKernelGGL((update_kernel<Op, DP, false, true>), grid, dim3(kThreads), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, false, true>), grid, dim3(Geo::THREADS), 0, s, p);
     else
-      hipLaunchKernelGGL((update_kernel<Op, DP, false, false>), grid, dim3(kThreads), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, false, false>), grid, dim3(Geo::THREADS), 0, s, p);
   }
   return hipGetLastError();
 }
