@@ -191,6 +191,23 @@ def test_device_resident_inputs_are_bit_identical_to_streamed(causal):
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
 
+@pytest.mark.parametrize("scale", [-0.2, 0.0, 1e-3])
+def test_negative_zero_and_tiny_softmax_scales(scale):
+    """The kernel folds a negative scale into the sign of Q and treats a zero
+    scale as 1e-30; both must reproduce softmax(scale * QK^T) V."""
+    announce(f"softmax scale {scale}")
+    gen = torch.Generator().manual_seed(53)
+    q = pinned_randn((300, 4, 128), torch.bfloat16, gen)
+    k = pinned_randn((500, 2, 128), torch.bfloat16, gen)
+    v = pinned_randn((500, 2, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 100, 300], dtype=torch.int32)
+    cu_k = torch.tensor([0, 240, 500], dtype=torch.int32)
+    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=128, kv_chunk_tokens=160)
+    out, lse, _ = run(q, k, v, cu_q, cu_k, config, causal=True, scale=scale)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=128, kv_chunk=160, causal=True, scale=scale)
+    check(out, lse, ref_o, ref_l)
+
+
 def test_repeated_runs_are_bit_identical():
     """Many workgroups per head and many K/V tiles per launch: three runs of
     the same inputs must agree bit for bit (a race between the LDS DMA of one
