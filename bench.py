@@ -76,12 +76,13 @@ def parse_args():
     ap.add_argument("--pinned-steps", type=int, default=None)
     ap.add_argument("--pinned-warmup", type=int, default=None)
     ap.add_argument("--traffic-file", type=Path, default=ROOT / "profiles" / "update_kernel_hbm_traffic.txt")
-    ap.add_argument("--workload", default="streamed", choices=["streamed", "paged", "sweep", "1m", "65k"],
+    ap.add_argument("--workload", default="streamed", choices=["streamed", "paged", "sweep", "1m", "65k", "projected"],
                     help="streamed: the headline 524,288-token run (default); paged: the 158,208-token "
                          "48-head paged run from an aligned on-disk page store; sweep: the 524,288-token "
                          "run from pinned DRAM at 1/2/4/8/14 GiB workspaces; 1m: 1,048,576 tokens x 64 "
                          "heads, peaked scores, 8 GiB workspace, with LSE; 65k: 65,536 tokens x 32 heads "
-                         "resident in HBM and streamed with 1 GiB")
+                         "resident in HBM and streamed with 1 GiB; projected: 61,312 tokens of hidden "
+                         "size 5,376 through QKV projection, attention and output projection")
     ap.add_argument("--store-dir", type=Path, default=None,
                     help="paged: directory for the temporary page store (default: $TMPDIR)")
     ap.add_argument("--direct-io", default="auto", choices=["auto", "on", "off"],
@@ -215,6 +216,8 @@ def main() -> int:
         return million_main(args)
     if args.workload == "65k":
         return small_main(args)
+    if args.workload == "projected":
+        return projected_main(args)
     legs = set(args.legs.split(","))
     if not legs <= {"resident", "pinned"} or not legs:
         print("--legs takes resident and/or pinned", file=sys.stderr)
@@ -644,6 +647,130 @@ def small_main(args) -> int:
     }
     print(json.dumps(result), flush=True)
     runner.close()
+    return 0 if (parity is None or parity["ok"]) else 1
+
+
+PROJ_TOKENS, PROJ_HIDDEN, PROJ_HEADS, PROJ_HEAD_DIM = 61_312, 5_376, 56, 128
+# Reference docs/projected_pipeline_benchmark.md:55 (pipeline mode, RTX 5090).
+REFERENCE_PROJECTED_MS = 843.44
+
+
+def projected_main(args) -> int:
+    """Hidden -> QKV projection -> streamed attention -> output projection at
+    the reference's projected-pipeline shape: 61,312 tokens, hidden 5,376,
+    56 heads x 128, bf16, non-causal, one segment, projection chunk 2,048,
+    K/V chunk 4,096, 2 GiB attention workspace, bias-free nn.Linear
+    projections.  Two residencies of the projected Q/K/V: pinned host memory
+    (the reference's schedule) and HBM."""
+    import numpy as np
+    import torch
+    from threadpoolctl import threadpool_limits
+
+    from oracle.seqattn_oracle import chunked_attention
+    from seqattn import (ProjectedAttentionRunner, ProjectedAttentionStats, ProjectionPipelineConfig,
+                         StreamingAttentionConfig, build_plan)
+
+    n, hid, h, d = PROJ_TOKENS, PROJ_HIDDEN, PROJ_HEADS, PROJ_HEAD_DIM
+    inner = h * d
+    gen = torch.Generator().manual_seed(args.seed)
+    hidden_cpu = torch.randn((n, hid), generator=gen).to(torch.bfloat16).pin_memory()
+    torch.manual_seed(args.seed + 1)
+    qkv_linear = torch.nn.Linear(hid, 3 * inner, bias=False, device="cuda", dtype=torch.bfloat16)
+    out_linear = torch.nn.Linear(inner, hid, bias=False, device="cuda", dtype=torch.bfloat16)
+
+    def project_qkv(hidden, start, stop):
+        qkv = qkv_linear(hidden).view(-1, h, 3, d)
+        return qkv[:, :, 0, :].contiguous(), qkv[:, :, 1, :].contiguous(), qkv[:, :, 2, :].contiguous()
+
+    def output_projector(attention, start, stop):
+        return out_linear(attention)
+
+    cu = torch.tensor([0, n], dtype=torch.int32)
+    attention_config = StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30, kv_chunk_tokens=4096,
+                                                num_output_buffers=2, backend="hip")
+    plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
+                      max_q_tokens=n, max_kv_tokens=n, config=attention_config)
+    attention_flop = 4 * h * d * n * n
+    gemm_flop = 2 * n * hid * 3 * inner + 2 * n * inner * hid
+    legs, outputs, runners = {}, {}, {}
+    for residency in ("host", "hbm"):
+        runner = ProjectedAttentionRunner(plan, attention_config, ProjectionPipelineConfig(
+            projection_chunk_tokens=2048, num_projection_buffers=2, qkv_residency=residency))
+        out = torch.empty((n, hid), dtype=torch.bfloat16, pin_memory=True)
+        with torch.inference_mode():
+            for _ in range(args.warmup):
+                runner(hidden_cpu, cu, project_qkv=project_qkv, output_projector=output_projector, out=out)
+            torch.cuda.synchronize()
+            stats = ProjectedAttentionStats()
+            t0 = time.perf_counter()
+            for _ in range(args.steps):
+                runner(hidden_cpu, cu, project_qkv=project_qkv, output_projector=output_projector, out=out,
+                       stats=stats)
+            torch.cuda.synchronize()
+        sec = (time.perf_counter() - t0) / args.steps
+        totals = stats.as_dict()
+        legs[residency] = {
+            "ms_per_call": round(sec * 1e3, 2),
+            "speedup_vs_reference": round(REFERENCE_PROJECTED_MS / (sec * 1e3), 2),
+            "projection_ms": round(stats.projection_seconds / args.steps * 1e3, 2),
+            "attention_and_output_ms": round(stats.attention_output_seconds / args.steps * 1e3, 2),
+            "attention_tflops_over_call": round(attention_flop / sec / 1e12, 1),
+            "logical_h2d_gib": round(totals["total_h2d_bytes"] / args.steps / 2**30, 3),
+            "logical_d2h_gib": round(totals["total_d2h_bytes"] / args.steps / 2**30, 3),
+            "peak_allocated_gib": round(torch.cuda.max_memory_allocated() / 2**30, 2),
+        }
+        log(f"projected {residency}: {legs[residency]}")
+        outputs[residency], runners[residency] = out, runner
+    host_runner = runners["host"]
+    parity = cpu_baseline = None
+    if not args.no_parity:
+        rng = np.random.default_rng(args.seed)
+        rows = np.unique(np.concatenate([[0, n // 4, n // 2, 3 * n // 4, n - 1],
+                                         rng.choice(n, args.parity_rows // 4, replace=False)]))
+        u16 = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+        q_rows = host_runner.q_cpu[:n][torch.from_numpy(rows)]
+        t0 = time.perf_counter()
+        with threadpool_limits(1):
+            ref_o, _ = chunked_attention(u16(q_rows), u16(host_runner.k_cpu[:n]), u16(host_runner.v_cpu[:n]),
+                                         [0, rows.size], [0, n], q_chunk_tokens=rows.size,
+                                         kv_chunk_tokens=4096, workers=args.cpu_workers)
+        cpu_s = time.perf_counter() - t0
+        attention_rows = torch.from_numpy(ref_o).to(torch.bfloat16).double().reshape(rows.size, inner)
+        expected = (attention_rows @ out_linear.weight.detach().cpu().double().t()).numpy()
+        parity = {"rows": int(rows.size)}
+        ok = True
+        for residency, out in outputs.items():
+            got = out[torch.from_numpy(rows)].double().numpy()
+            diff = np.abs(got - expected)
+            norm = float(np.linalg.norm(expected))
+            rms = norm / math.sqrt(expected.size)
+            leg = {"max_abs": float(diff.max()), "rel_l2": float(np.linalg.norm(diff)) / norm,
+                   "max_scaled_err": float((diff / (np.abs(expected) + rms)).max())}
+            parity[residency] = leg
+            ok = ok and leg["rel_l2"] <= 1e-2 and leg["max_scaled_err"] <= 2.0**-5
+        parity["host_and_hbm_bit_identical"] = bool(torch.equal(outputs["host"], outputs["hbm"]))
+        parity["ok"] = bool(ok and parity["host_and_hbm_bit_identical"])
+        cpu_baseline = {"value": 4 * h * d * rows.size * n / cpu_s / 1e12, "unit": "TFLOPS",
+                        "cores": args.cpu_workers, "kind": "port",
+                        "sample": f"attention of {rows.size} query rows x {h} heads x all {n} keys; {cpu_s:.2f} s"}
+        log(f"projected parity: {parity}")
+    best = min(legs.values(), key=lambda leg: leg["ms_per_call"])
+    result = {
+        "metric": "latency, 61K-token projected self-attention (hidden 5,376 -> QKV -> attention -> out_proj)",
+        "value": best["ms_per_call"], "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": best["ms_per_call"], "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic: hidden ~ N(0,1) bf16 pinned; nn.Linear default-initialised bf16 projections",
+        "config": {"workload": f"{n:,} tokens, hidden {hid:,}, {h} heads x {d}, non-causal, one segment, "
+                               "projection chunk 2,048, K/V chunk 4,096, 2 GiB attention workspace",
+                   "q_chunk_tokens": plan.q_chunk_tokens, "q_passes": plan.q_passes,
+                   "qkv_and_out_projection_tflop": round(gemm_flop / 1e12, 2)},
+        "reference_rtx5090_ms": REFERENCE_PROJECTED_MS,
+        "legs": legs,
+        "cpu_baseline": cpu_baseline,
+        "parity": parity,
+    }
+    print(json.dumps(result), flush=True)
     return 0 if (parity is None or parity["ok"]) else 1
 
 

@@ -6,11 +6,12 @@ Drop-in for the reference package's tensor-mode and device-consumer API
 HBM workspace; the chunk-update / finalize kernels and the copy pipeline are
 native gfx950 code in ``_lib/libseqattn_hip.so``.  Paged mode
 (``PagedAttentionRunner`` over memory or aligned on-disk page stores) runs on
-the same kernels and pipeline.
+the same kernels and pipeline, and ``ProjectedAttentionRunner`` fuses a
+caller's QKV and output projections around the streamed attention.
 """
 
 from .api import StreamingAttentionRunner, streaming_attn_func, streaming_attn_varlen_func
-from .config import PagedAttentionConfig, StreamingAttentionConfig
+from .config import PagedAttentionConfig, ProjectionPipelineConfig, StreamingAttentionConfig
 from .paged import (
     CallbackOutputSink,
     HostMemoryPlan,
@@ -25,6 +26,12 @@ from .paged import (
     TensorLayout,
 )
 from .planner import AttentionPlan, build_plan
+from .projection import (
+    OutputProjector,
+    ProjectedAttentionRunner,
+    QKVProjector,
+    streaming_projected_self_attention,
+)
 from .stats import PagedAttentionStats, ProjectedAttentionStats, StreamingAttentionStats
 from .storage import NvmeOutputSink, NvmeQKVStore, NvmeQKVWriter, ephemeral_nvme_directory, load_nvme_output
 
@@ -39,13 +46,17 @@ __all__ = [
     "NvmeOutputSink",
     "NvmeQKVStore",
     "NvmeQKVWriter",
+    "OutputProjector",
     "PageDescriptor",
     "PageSink",
     "PageSource",
     "PagedAttentionConfig",
     "PagedAttentionRunner",
     "PagedAttentionStats",
+    "ProjectedAttentionRunner",
     "ProjectedAttentionStats",
+    "ProjectionPipelineConfig",
+    "QKVProjector",
     "StreamingAttentionConfig",
     "StreamingAttentionRunner",
     "StreamingAttentionStats",
@@ -55,6 +66,7 @@ __all__ = [
     "load_nvme_output",
     "streaming_attn_func",
     "streaming_attn_varlen_func",
+    "streaming_projected_self_attention",
 ]
 
 __version__ = "0.3.0+mi355x"

@@ -39,7 +39,8 @@ class StreamingAttentionConfig:
     # setting any one switches to the portable 64x64/4/2 baseline with the
     # supplied values as overrides.  block_m / block_n set the alignment of the
     # planned Q and K/V chunks; the gfx950 kernel's own tile geometry is fixed
-    # (128 queries x 64 keys, 4 wavefronts, register+LDS double buffering).
+    # (256 queries x 64 keys per workgroup for head_dim <= 128, K/V tiles
+    # double-buffered in LDS).
     block_m: int | None = None
     block_n: int | None = None
     num_warps: int | None = None
@@ -137,4 +138,45 @@ class PagedAttentionConfig:
             raise ValueError("V1 INT8 storage requires quant_group_tokens=64")
 
 
-__all__ = ["BACKENDS", "OUTPUT_MODES", "PagedAttentionConfig", "StreamingAttentionConfig"]
+QKV_RESIDENCIES = {"host", "hbm"}
+
+
+@dataclass(frozen=True)
+class ProjectionPipelineConfig:
+    """Policy of the hidden -> QKV -> attention -> output projection pipeline
+    (reference src/seqattn_core/config.py:122-142).
+
+    Exact self-attention needs every K/V row before any query can finish, so
+    the QKV projection runs as a chunked producer phase, then attention with
+    the output projection fused onto each finalized tile.  Additive option:
+    ``qkv_residency="hbm"`` keeps the projected Q/K/V in device memory
+    instead of staging them in pinned host buffers; attention then reads
+    them in place (no Q/K/V PCIe traffic at all) and only the projected
+    output crosses the link.
+    """
+
+    projection_chunk_tokens: int = 2048
+    num_projection_buffers: int = 2
+    require_pinned_hidden: bool = True
+    pin_qkv: bool = True
+    pin_output: bool = True
+    enable_nvtx: bool = False
+    qkv_residency: str = "host"
+
+    def validate(self) -> None:
+        if self.projection_chunk_tokens <= 0:
+            raise ValueError("projection_chunk_tokens must be positive")
+        if self.num_projection_buffers not in {1, 2, 3}:
+            raise ValueError("num_projection_buffers must be 1, 2, or 3")
+        if self.qkv_residency not in QKV_RESIDENCIES:
+            raise ValueError("qkv_residency must be 'host' or 'hbm'")
+
+
+__all__ = [
+    "BACKENDS",
+    "OUTPUT_MODES",
+    "PagedAttentionConfig",
+    "ProjectionPipelineConfig",
+    "QKV_RESIDENCIES",
+    "StreamingAttentionConfig",
+]

@@ -4,8 +4,8 @@
 the reference wrappers (src/seqattn_core/kernels/streaming.py:205-271 and
 :345-371) and launch asynchronously on torch's current stream.  The launch
 parameters block_m/block_n/num_warps/num_stages are accepted for
-compatibility; the gfx950 kernel uses its own fixed tile (128 queries x 64
-keys, 4 wavefronts).  ``finalize_attention`` gains optional ``running_max`` /
+compatibility; the gfx950 kernel uses its own fixed tile (256 queries x 64
+keys per workgroup for head_dim <= 128).  ``finalize_attention`` gains optional ``running_max`` /
 ``lse`` arguments that write the natural-log LSE ``[heads, tokens]``.
 """
 

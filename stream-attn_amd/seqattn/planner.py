@@ -13,10 +13,12 @@ kv_chunk_tokens and estimated bytes (pinned against the reference README's
 * ``_candidate_cost`` (L158-184): PCIe / state-traffic / launch cost model
   used to pick the K/V chunk jointly with Q.
 
-gfx950 specifics: on a ROCm device the launch preset is the native kernel's
-real tile (128 queries x 64 keys, 4 wavefronts, 2 stages) for every head_dim,
-and ``output_mode="host_aliased"`` charges no raw output slots because the
-output is finalized into the Q buffer.
+gfx950 specifics: on a ROCm device the launch preset is (128, 64, 4, 2) for
+every head_dim: Q chunks align to 128 rows and K/V chunks to the kernel's
+64-key LDS tile (a workgroup covers 256 queries for head_dim <= 128, and
+the last workgroup of a chunk is masked, so 128-row alignment costs at most
+half a workgroup per chunk).  ``output_mode="host_aliased"`` charges no raw
+output slots because the output is finalized into the Q buffer.
 """
 
 from __future__ import annotations
