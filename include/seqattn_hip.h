@@ -82,6 +82,39 @@ int32_t sa_update_attention_state(
     void* stream);
 
 /*
+ * The update above with INT8 K/V and per-group fp16 scales.
+ *
+ * Replaces update_attention_state_int8 (reference
+ * src/seqattn_core/kernels/streaming.py:274-342; dequantization at lines 113-120).
+ *
+ *   k, v     [kv_tokens, kv_heads, head_dim] int8, strides (stride_kt, stride_kh, 1), multiples of 16
+ *   k_scales, v_scales  fp16, element (g, h) at scales[g * stride_?sg + h * stride_?sh]
+ *
+ * Key j of K/V head h is dequantized as dtype(float(k[j, h, :]) * float(scale))
+ * with scale = k_scales[(storage_token_offset + j) / quant_group_tokens, h]
+ * (quant_group_tokens a power of two; the reference's pages use 64), which is
+ * the reference's rounding: the result equals sa_update_attention_state on the
+ * dequantized K/V.  head_dim is a multiple of 16 in [16, 128].  Other
+ * arguments as in sa_update_attention_state.
+ */
+int32_t sa_update_attention_state_int8(
+    const void* q, const void* k, const void* v,
+    const void* k_scales, const void* v_scales,
+    float* running_max, float* running_sum, float* accumulator,
+    int64_t stride_qt, int64_t stride_qh,
+    int64_t stride_kt, int64_t stride_kh,
+    int64_t stride_vt, int64_t stride_vh,
+    int64_t stride_ksg, int64_t stride_ksh,
+    int64_t stride_vsg, int64_t stride_vsh,
+    int64_t stride_st, int64_t stride_sh,
+    int64_t stride_at, int64_t stride_ah,
+    int32_t q_tokens, int32_t kv_tokens,
+    int32_t q_heads, int32_t kv_heads, int32_t head_dim,
+    int32_t q_local_offset, int32_t kv_local_offset, int32_t storage_token_offset,
+    int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
+    int32_t quant_group_tokens, void* stream);
+
+/*
  * out = acc / l where l > 0, else 0, cast to dtype; optionally
  * lse = ln(sum exp(logits)) = (m + log2 l) * ln 2 (natural log), -inf where l == 0.
  *

@@ -14,6 +14,11 @@ the reference file:line it follows.  Parity pins (see tests/test_oracle.py):
   brute-force per-row float64 loop on tiny inputs, and across chunk sizes
   (chunking must not change the result beyond fp32 rounding).
 * ``chunked_attention_rows`` equals ``chunked_attention`` on the same rows.
+* ``quantize_int8_groups`` / ``dequantize_int8_groups`` /
+  ``round_f32_to_bf16_bits`` against hand-worked known answers (exact
+  integer groups, all-zero groups, ties rounding to even, clamping, the
+  float16 scale), the reconstruction bound |x - deq| <= step / 2 (+ scale
+  rounding), torch's own bfloat16 conversion, and the group offset rule.
 * ``seeded_normal_chunks`` reproduces torch's generator stream exactly (it
   calls torch's CPU generator, the same calls the reference's benchmark
   makes) and is checked element-for-element against a direct torch call.
@@ -270,8 +275,60 @@ def seeded_normal_chunks(tokens: int, heads: int, head_dim: int, *, seed: int, t
     return out
 
 
+def round_f32_to_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """bfloat16 bit patterns (uint16) of float32 values, round to nearest even
+    (the conversion torch and the reference kernels use); NaN stays NaN."""
+    bits = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32)
+    rounded = bits + np.uint32(0x7FFF) + ((bits >> 16) & np.uint32(1))
+    out = (rounded >> 16).astype(np.uint16)
+    nan = np.isnan(x)
+    if nan.any():
+        out[nan] = np.uint16(0x7FC0)
+    return out
+
+
+def quantize_int8_groups(x: np.ndarray, group_tokens: int = 64) -> tuple[np.ndarray, np.ndarray]:
+    """Symmetric INT8 storage of ``x [tokens, heads, head_dim]`` (float32 view).
+
+    Follows quantize_int8_per_token_group (reference
+    src/seqattn_core/quantization.py:8-35): per group of ``group_tokens`` rows
+    and per head, step = amax / 127 in float32 (1 where amax is 0),
+    q = clamp(round_half_even(x / step), -127, 127), and the stored scale is
+    float16(step).  Returns (q int8, scales float16 [groups, heads]).
+    """
+    x = as_f32(np.asarray(x))
+    tokens, heads, _ = x.shape
+    groups = -(-tokens // group_tokens)
+    q = np.empty(x.shape, dtype=np.int8)
+    scales = np.empty((groups, heads), dtype=np.float16)
+    for g in range(groups):
+        block = x[g * group_tokens : min((g + 1) * group_tokens, tokens)]
+        step = (np.abs(block).max(axis=(0, 2)) / np.float32(127.0)).astype(np.float32)
+        step = np.where(step > 0, step, np.float32(1.0)).astype(np.float32)
+        scales[g] = step.astype(np.float16)
+        q[g * group_tokens : g * group_tokens + block.shape[0]] = np.clip(
+            np.round(block / step[None, :, None]), -127, 127).astype(np.int8)
+    return q, scales
+
+
+def dequantize_int8_groups(q: np.ndarray, scales: np.ndarray, *, group_tokens: int = 64,
+                           token_offset: int = 0, to_bf16: bool = True) -> np.ndarray:
+    """Dequantized K or V as the reference's INT8 update kernel forms it
+    (reference src/seqattn_core/kernels/streaming.py:113-120): row j uses
+    scale[(token_offset + j) // group_tokens]; the product float32(q) *
+    float32(scale) is rounded once in float32 and then to the query dtype.
+    Returns bf16 bit patterns (uint16) by default, else the float32 product."""
+    q = np.asarray(q)
+    rows = (token_offset + np.arange(q.shape[0])) // group_tokens
+    product = q.astype(np.float32) * np.asarray(scales, dtype=np.float16).astype(np.float32)[rows][:, :, None]
+    return round_f32_to_bf16_bits(product) if to_bf16 else product
+
+
 __all__ = [
     "brute_force_row",
+    "dequantize_int8_groups",
+    "quantize_int8_groups",
+    "round_f32_to_bf16_bits",
     "chunked_attention",
     "dense_attention_f64",
     "seeded_normal_chunks",

@@ -59,6 +59,16 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
                       hipStream_t stream);
+int32_t launch_update_int8(const void* q, const void* k, const void* v, const void* k_scales,
+                           const void* v_scales, float* m, float* l, float* acc, int64_t sq_t,
+                           int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t, int64_t sv_h,
+                           int64_t sks_g, int64_t sks_h, int64_t svs_g, int64_t svs_h,
+                           int64_t ss_t, int64_t ss_h, int64_t sa_t, int64_t sa_h,
+                           int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
+                           int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
+                           int32_t storage_token_offset, int32_t causal_shift,
+                           double softmax_scale, int32_t flags, int32_t dtype,
+                           int32_t quant_group_tokens, hipStream_t stream);
 int32_t launch_finalize(const float* acc, const float* m, const float* l, void* out, float* lse,
                         int64_t sa_t, int64_t sa_h, int64_t ss_t, int64_t ss_h, int64_t so_t,
                         int64_t so_h, int64_t lse_sh, int64_t lse_off, int32_t q_tokens,

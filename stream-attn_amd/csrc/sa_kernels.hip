@@ -45,6 +45,16 @@
 // out = acc / l and LSE = m + log2(l) are unchanged, and P keeps bf16's
 // relative precision.  The row sum l is accumulated per lane half and the two
 // halves are combined once when the state is written.
+//
+// INT8 K/V (update_attention_state_int8, reference kernels/streaming.py:113-120
+// and :274-342): int8 rows with one fp16 scale per (token group, K/V head).
+// Raw int8 tiles (half the bytes of bf16) arrive by LDS DMA into a staging
+// area; one pass per tile turns them into the bf16/fp16 stage layout above as
+// dtype(fp32(k) * fp32(scale)), exactly the reference's dequantization, so
+// the MFMA loop is shared and the result equals the 16-bit kernel run on
+// dequantized K/V bit for bit.  Per tile: DMA of tile t+2, dequantization of
+// tile t+1 and the MFMAs of tile t, one barrier.  Each thread's scales for
+// the next tile are loaded into registers one tile ahead.
 
 #include <hip/hip_runtime.h>
 
@@ -107,6 +117,12 @@ struct UpdateParams {
   int32_t q_blocks;       // workgroups per query head
   int32_t xcd_run;        // ceil(q_blocks * q_heads / 8)
   float scale_log2;
+  // INT8 K/V only: fp16 scales, element (group, kv_head) at
+  // scales[group * s?s_g + kv_head * s?s_h], group = (scale_offset + key) >> scale_shift.
+  const uint16_t* ks;
+  const uint16_t* vs;
+  int64_t sks_g, sks_h, svs_g, svs_h;
+  int32_t scale_offset, scale_shift;
 };
 
 // Row r (0..15) of a 32x32 C tile held in register i of a lane in half h.
@@ -144,6 +160,14 @@ struct Geometry {
   static constexpr int KB = DP == 128 ? 2 : DP / 16;
   static constexpr int VB = DP == 128 ? 2 : (DP / 32 < 4 ? DP / 32 : 4);
   static_assert(DMA_PER_WAVE >= 1, "tile too small for the workgroup");
+  // INT8 staging: a tile is 64 rows of DP bytes; a wave-wide 16-byte-per-lane
+  // DMA moves 1 KB, I8_GR granules of 16 int8 per row.
+  static constexpr int I8_TILE_BYTES = TILE_KEYS * DP;
+  static constexpr int I8_GR = DP / 16;
+  static constexpr int I8_DMAS = I8_TILE_BYTES / 1024;                // per tensor per tile
+  static constexpr int I8_DMA_PER_WAVE = (I8_DMAS + WAVES - 1) / WAVES;
+  static constexpr int I8_GRANULES = TILE_KEYS * I8_GR;               // per tensor per tile
+  static constexpr int I8_PER_THREAD = (I8_GRANULES + THREADS - 1) / THREADS;
   // Granule swizzle: rows r..r+7 (r % 8 == 0) get 8 distinct XOR masks and
   // rows r..r+3 (r % 4 == 0) masks that differ in bits 1-2.
   __device__ static inline int swz(int row) { return (((row & 3) << 1) | ((row >> 2) & 1)) & (G - 1); }
@@ -152,7 +176,7 @@ struct Geometry {
   }
 };
 
-template <typename Op, int DP, bool CAUSAL, bool INIT>
+template <typename Op, int DP, bool CAUSAL, bool INIT, bool QUANT>
 __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const UpdateParams p) {
   using Geo = Geometry<DP>;
   constexpr int QB = Geo::QB;
@@ -166,6 +190,10 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
   // need not wait for it.
   __shared__ __attribute__((aligned(1024))) uint8_t lds_a[2 * Geo::TILE_BYTES];
   __shared__ __attribute__((aligned(1024))) uint8_t lds_b[2 * Geo::TILE_BYTES];
+  // INT8 staging (K then V of one raw tile), also two distinct objects.
+  constexpr int kStagingBytes = QUANT ? 2 * Geo::I8_TILE_BYTES : 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_qa[kStagingBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_qb[kStagingBytes];
 
   // XCD-aware numbering: hardware block b runs on XCD b % 8; consecutive
   // logical workgroups (same head, neighbouring query blocks) share an XCD.
@@ -289,17 +317,9 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
     }
   };
 
-  // Tile t is computed from `cur` while tile t+1 streams into `next`.
-  auto tile = [&](int t, const uint8_t* cur, uint8_t* next) {
+  // The MFMA / softmax work of tile t, read from the 16-bit stage `cur`.
+  auto compute = [&](int t, const uint8_t* cur) {
     const int kt = t * Geo::TILE_KEYS;
-    // Every wave waits for its own DMA of tile t before the barrier, so after
-    // it all 64 rows of `cur` are in LDS.  LDS DMA is counted by vmcnt, which
-    // a workgroup-scope fence does not wait for: without this explicit wait a
-    // wave could read rows that another wave's DMA has not written yet.  The
-    // barrier also guarantees `next` (tile t-1) is no longer being read.
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    if (t + 1 < ntiles) issue_tile(kt + Geo::TILE_KEYS, next);
     const uint8_t* k_stage = cur;
     const uint8_t* v_stage = cur + Geo::TILE_BYTES;
 
@@ -442,10 +462,139 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
     }
   };
 
-  if (ntiles > 0) issue_tile(0, lds_a);
-  for (int t = 0; t < ntiles; t += 2) {
-    tile(t, lds_a, lds_b);
-    if (t + 1 < ntiles) tile(t + 1, lds_b, lds_a);
+  if constexpr (!QUANT) {
+    // Tile t is computed from `cur` while tile t+1 streams into `next`.
+    auto tile = [&](int t, const uint8_t* cur, uint8_t* next) {
+      // Every wave waits for its own DMA of tile t before the barrier, so
+      // after it all 64 rows of `cur` are in LDS.  LDS DMA is counted by
+      // vmcnt, which a workgroup-scope fence does not wait for: without this
+      // explicit wait a wave could read rows that another wave's DMA has not
+      // written yet.  The barrier also guarantees `next` (tile t-1) is no
+      // longer being read.
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (t + 1 < ntiles) issue_tile((t + 1) * Geo::TILE_KEYS, next);
+      compute(t, cur);
+    };
+    if (ntiles > 0) issue_tile(0, lds_a);
+    for (int t = 0; t < ntiles; t += 2) {
+      tile(t, lds_a, lds_b);
+      if (t + 1 < ntiles) tile(t + 1, lds_b, lds_a);
+    }
+  } else {
+    // Raw int8 tile [kt, kt + 64) of K and V into staging `stg` (K at 0, V at
+    // I8_TILE_BYTES), row-major with 16-byte granules; the same tail and
+    // head_dim clamps as the 16-bit path keep every address in the buffers.
+    const uint8_t* kp8 = reinterpret_cast<const uint8_t*>(p.k) + (int64_t)kv_head * p.sk_h;
+    const uint8_t* vp8 = reinterpret_cast<const uint8_t*>(p.v) + (int64_t)kv_head * p.sv_h;
+    int k8_off[Geo::I8_DMA_PER_WAVE], v8_off[Geo::I8_DMA_PER_WAVE], row8[Geo::I8_DMA_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < Geo::I8_DMA_PER_WAVE; ++i) {
+      const int chunk = wave + Geo::WAVES * i;
+      const int row = chunk * (1024 / DP) + lane / Geo::I8_GR;
+      const int gr = lane % Geo::I8_GR;
+      const int col = gr * 16 < p.head_dim ? gr * 16 : 0;
+      row8[i] = row;
+      k8_off[i] = row * (int)p.sk_t + col;
+      v8_off[i] = row * (int)p.sv_t + col;
+    }
+    auto issue_i8 = [&](int kt, uint8_t* stg) {
+      const uint8_t* kt_base = kp8 + (int64_t)kt * p.sk_t;
+      const uint8_t* vt_base = vp8 + (int64_t)kt * p.sv_t;
+#pragma unroll
+      for (int i = 0; i < Geo::I8_DMA_PER_WAVE; ++i) {
+        const int chunk = wave + Geo::WAVES * i;
+        if (Geo::I8_DMAS % Geo::WAVES != 0 && chunk >= Geo::I8_DMAS) break;
+        int ko = k8_off[i], vo = v8_off[i];
+        if (kt + row8[i] >= p.kv_tokens) {
+          const int back = kt + row8[i] - (p.kv_tokens - 1);
+          ko -= back * (int)p.sk_t;
+          vo -= back * (int)p.sv_t;
+        }
+        __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kt_base + ko),
+                                         (SA_LDS void*)(stg + chunk * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(vt_base + vo),
+                                         (SA_LDS void*)(stg + Geo::I8_TILE_BYTES + chunk * 1024), 16, 0, 0);
+      }
+    };
+    // This thread's dequantization granules: g = tid + THREADS * j, row g / I8_GR.
+    // Their scales (raw fp16 bits) are loaded one tile ahead into registers.
+    uint32_t ksc[Geo::I8_PER_THREAD], vsc[Geo::I8_PER_THREAD];
+    const uint16_t* ksp = p.ks + (int64_t)kv_head * p.sks_h;
+    const uint16_t* vsp = p.vs + (int64_t)kv_head * p.svs_h;
+    auto load_scales = [&](int kt) {
+#pragma unroll
+      for (int j = 0; j < Geo::I8_PER_THREAD; ++j) {
+        const int g = tid + Geo::THREADS * j;
+        const int key = min(kt + min(g, Geo::I8_GRANULES - 1) / Geo::I8_GR, p.kv_tokens - 1);
+        const int64_t group = (int64_t)((p.scale_offset + key) >> p.scale_shift);
+        ksc[j] = ksp[group * p.sks_g];
+        vsc[j] = vsp[group * p.svs_g];
+      }
+    };
+    // dtype(fp32(k) * fp32(scale)) into the swizzled 16-bit stage.  A signed
+    // byte b is (b ^ 0x80) - 128; fma(u, s, -128 s) rounds (u - 128) * s once,
+    // the same value as the reference's fp32 product.
+    auto dequant = [&](const uint8_t* stg, uint8_t* stage) {
+#pragma unroll
+      for (int j = 0; j < Geo::I8_PER_THREAD; ++j) {
+        const int g = tid + Geo::THREADS * j;
+        if (Geo::I8_GRANULES % Geo::THREADS != 0 && g >= Geo::I8_GRANULES) break;
+        const int row = g / Geo::I8_GR;
+        const int gr = g % Geo::I8_GR;
+#pragma unroll
+        for (int tensor = 0; tensor < 2; ++tensor) {
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(stg + tensor * Geo::I8_TILE_BYTES + row * DP + gr * 16);
+          const uint16_t bits = (uint16_t)(tensor == 0 ? ksc[j] : vsc[j]);
+          const float sc = (float)__builtin_bit_cast(_Float16, bits);
+          const float nb = -128.f * sc;
+          u32x4 out[2];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t x = raw[w] ^ 0x80808080u;
+            const float f0 = fmaf((float)(x & 0xffu), sc, nb);
+            const float f1 = fmaf((float)((x >> 8) & 0xffu), sc, nb);
+            const float f2 = fmaf((float)((x >> 16) & 0xffu), sc, nb);
+            const float f3 = fmaf((float)(x >> 24), sc, nb);
+            out[w >> 1][2 * (w & 1)] = Op::pack2(f0, f1);
+            out[w >> 1][2 * (w & 1) + 1] = Op::pack2(f2, f3);
+          }
+          uint8_t* dst = stage + tensor * Geo::TILE_BYTES;
+          *reinterpret_cast<u32x4*>(dst + Geo::offset(row, 2 * gr)) = out[0];
+          *reinterpret_cast<u32x4*>(dst + Geo::offset(row, 2 * gr + 1)) = out[1];
+        }
+      }
+    };
+    // At tile t: `cur` holds tile t (dequantized before the barrier), staging
+    // `stg_next` holds raw tile t+1 and `stg_cur` (raw tile t) and `next`
+    // (read by tile t-1's MFMAs) are free.  The vmcnt wait covers this wave's
+    // DMA and scale loads; the barrier makes every wave's DMA and
+    // dequantization writes visible.
+    auto tile_q = [&](int t, const uint8_t* cur, uint8_t* next, uint8_t* stg_cur, const uint8_t* stg_next) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (t + 2 < ntiles) issue_i8((t + 2) * Geo::TILE_KEYS, stg_cur);
+      if (t + 1 < ntiles) {
+        dequant(stg_next, next);
+        if (t + 2 < ntiles) load_scales((t + 2) * Geo::TILE_KEYS);
+      }
+      compute(t, cur);
+    };
+    if (ntiles > 0) {
+      issue_i8(0, lds_qa);
+      load_scales(0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      dequant(lds_qa, lds_a);
+      if (ntiles > 1) {
+        issue_i8(Geo::TILE_KEYS, lds_qb);
+        load_scales(Geo::TILE_KEYS);
+      }
+    }
+    for (int t = 0; t < ntiles; t += 2) {
+      tile_q(t, lds_a, lds_b, lds_qa, lds_qb);
+      if (t + 1 < ntiles) tile_q(t + 1, lds_b, lds_a, lds_qb, lds_qa);
+    }
   }
 
 #pragma unroll
@@ -513,7 +662,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
   }
 }
 
-template <typename Op, int DP>
+template <typename Op, int DP, bool QUANT>
 hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t s) {
   using Geo = Geometry<DP>;
   p.q_blocks = (p.q_tokens + Geo::BLOCK_M - 1) / Geo::BLOCK_M;
@@ -522,14 +671,14 @@ hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t 
   const dim3 grid((unsigned)(8 * (int64_t)p.xcd_run));
   if (causal) {
     if (init)
-      hipLaunchKernelGGL((update_kernel<Op, DP, true, true>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, true, true, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
     else
-      hipLaunchKernelGGL((update_kernel<Op, DP, true, false>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, true, false, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
   } else {
     if (init)
-      hipLaunchKernelGGL((update_kernel<Op, DP, false, true>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, false, true, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
     else
-      hipLaunchKernelGGL((update_kernel<Op, DP, false, false>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update_kernel<Op, DP, false, false, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
   }
   return hipGetLastError();
 }
@@ -537,10 +686,21 @@ hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t 
 template <typename Op>
 hipError_t launch_update_op(const UpdateParams& p, int dp, bool causal, bool init, hipStream_t s) {
   switch (dp) {
-    case 32: return launch_update_dp<Op, 32>(p, causal, init, s);
-    case 64: return launch_update_dp<Op, 64>(p, causal, init, s);
-    case 128: return launch_update_dp<Op, 128>(p, causal, init, s);
-    default: return launch_update_dp<Op, 256>(p, causal, init, s);
+    case 32: return launch_update_dp<Op, 32, false>(p, causal, init, s);
+    case 64: return launch_update_dp<Op, 64, false>(p, causal, init, s);
+    case 128: return launch_update_dp<Op, 128, false>(p, causal, init, s);
+    default: return launch_update_dp<Op, 256, false>(p, causal, init, s);
+  }
+}
+
+// INT8 K/V covers head_dim <= 128: with head_dim 256 the 16-bit stages and the
+// raw staging would not fit in LDS together.
+template <typename Op>
+hipError_t launch_update_int8_op(const UpdateParams& p, int dp, bool causal, bool init, hipStream_t s) {
+  switch (dp) {
+    case 32: return launch_update_dp<Op, 32, true>(p, causal, init, s);
+    case 64: return launch_update_dp<Op, 64, true>(p, causal, init, s);
+    default: return launch_update_dp<Op, 128, true>(p, causal, init, s);
   }
 }
 
@@ -620,6 +780,91 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
   return err == hipSuccess ? 0 : hip_status(err, "update kernel launch");
 }
 
+int32_t launch_update_int8(const void* q, const void* k, const void* v, const void* k_scales,
+                           const void* v_scales, float* m, float* l, float* acc, int64_t sq_t,
+                           int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t, int64_t sv_h,
+                           int64_t sks_g, int64_t sks_h, int64_t svs_g, int64_t svs_h,
+                           int64_t ss_t, int64_t ss_h, int64_t sa_t, int64_t sa_h,
+                           int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
+                           int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
+                           int32_t storage_token_offset, int32_t causal_shift,
+                           double softmax_scale, int32_t flags, int32_t dtype,
+                           int32_t quant_group_tokens, hipStream_t stream) {
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
+    set_error("sa_update_attention_state_int8: unsupported query dtype code %d", dtype);
+    return SA_ERR_UNSUPPORTED_DTYPE;
+  }
+  if (head_dim < 16 || head_dim > 128 || head_dim % 16 != 0) {
+    set_error("sa_update_attention_state_int8: head_dim must be a multiple of 16 in [16, 128], got %d",
+              head_dim);
+    return SA_ERR_UNSUPPORTED_HEAD_DIM;
+  }
+  if (q_tokens < 0 || kv_tokens < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 ||
+      storage_token_offset < 0) {
+    set_error("sa_update_attention_state_int8: bad sizes q_tokens=%d kv_tokens=%d q_heads=%d kv_heads=%d "
+              "storage_token_offset=%d", q_tokens, kv_tokens, q_heads, kv_heads, storage_token_offset);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  int shift = 0;
+  while (shift < 30 && (1 << shift) < quant_group_tokens) ++shift;
+  if (quant_group_tokens <= 0 || (1 << shift) != quant_group_tokens) {
+    set_error("sa_update_attention_state_int8: quant_group_tokens must be a power of two, got %d",
+              quant_group_tokens);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (q_tokens == 0) return 0;
+  if (!q || !k || !v || !k_scales || !v_scales || !m || !l || !acc) {
+    set_error("sa_update_attention_state_int8: null pointer argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  // Q: 16-byte vectors of 8 elements; int8 K/V: 16-byte DMA granules.
+  if (sq_t % 8 != 0 || sq_h % 8 != 0 || sk_t % 16 != 0 || sk_h % 16 != 0 || sv_t % 16 != 0 ||
+      sv_h % 16 != 0) {
+    set_error("sa_update_attention_state_int8: q strides must be multiples of 8 elements and int8 "
+              "k/v strides multiples of 16");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (sk_t <= 0 || sv_t <= 0 || sk_t >= (1 << 24) || sv_t >= (1 << 24)) {
+    set_error("sa_update_attention_state_int8: k/v token strides must be in [1, 2^24) elements");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (sa_t % 4 != 0 || sa_h % 4 != 0 || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) ||
+      !aligned(acc, 16) || !aligned(m, 4) || !aligned(l, 4) || !aligned(k_scales, 2) ||
+      !aligned(v_scales, 2)) {
+    set_error("sa_update_attention_state_int8: buffers must be aligned (16 bytes for q/k/v/acc, 2 for scales)");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  UpdateParams p;
+  p.q = static_cast<const uint16_t*>(q);
+  p.k = static_cast<const uint16_t*>(k);
+  p.v = static_cast<const uint16_t*>(v);
+  p.m = m;
+  p.l = l;
+  p.acc = acc;
+  p.sq_t = sq_t; p.sq_h = sq_h; p.sk_t = sk_t; p.sk_h = sk_h; p.sv_t = sv_t; p.sv_h = sv_h;
+  p.ss_t = ss_t; p.ss_h = ss_h; p.sa_t = sa_t; p.sa_h = sa_h;
+  p.q_tokens = q_tokens;
+  p.kv_tokens = kv_tokens;
+  p.group = q_heads / kv_heads;
+  p.head_dim = head_dim;
+  p.q_local_offset = q_local_offset;
+  p.kv_local_offset = kv_local_offset;
+  p.causal_shift = causal_shift;
+  p.scale_log2 = (float)(softmax_scale * 1.4426950408889634);
+  p.q_heads = q_heads;
+  p.ks = static_cast<const uint16_t*>(k_scales);
+  p.vs = static_cast<const uint16_t*>(v_scales);
+  p.sks_g = sks_g; p.sks_h = sks_h; p.svs_g = svs_g; p.svs_h = svs_h;
+  p.scale_offset = storage_token_offset;
+  p.scale_shift = shift;
+  const int dp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : 128;
+  const bool causal = (flags & SA_FLAG_CAUSAL) != 0;
+  const bool init = (flags & SA_FLAG_INITIALIZE) != 0;
+  hipError_t err = dtype == SA_DTYPE_BF16 ? launch_update_int8_op<BF16>(p, dp, causal, init, stream)
+                                          : launch_update_int8_op<FP16>(p, dp, causal, init, stream);
+  return err == hipSuccess ? 0 : hip_status(err, "int8 update kernel launch");
+}
+
 int32_t launch_finalize(const float* acc, const float* m, const float* l, void* out, float* lse,
                         int64_t sa_t, int64_t sa_h, int64_t ss_t, int64_t ss_h, int64_t so_t,
                         int64_t so_h, int64_t lse_sh, int64_t lse_off, int32_t q_tokens,
@@ -686,6 +931,25 @@ int32_t sa_update_attention_state(const void* q, const void* k, const void* v, f
                            stride_at, stride_ah, q_tokens, kv_tokens, q_heads, kv_heads, head_dim,
                            q_local_offset, kv_local_offset, causal_shift, softmax_scale, flags,
                            dtype, static_cast<hipStream_t>(stream));
+}
+
+int32_t sa_update_attention_state_int8(
+    const void* q, const void* k, const void* v, const void* k_scales, const void* v_scales,
+    float* running_max, float* running_sum, float* accumulator, int64_t stride_qt,
+    int64_t stride_qh, int64_t stride_kt, int64_t stride_kh, int64_t stride_vt, int64_t stride_vh,
+    int64_t stride_ksg, int64_t stride_ksh, int64_t stride_vsg, int64_t stride_vsh,
+    int64_t stride_st, int64_t stride_sh, int64_t stride_at, int64_t stride_ah, int32_t q_tokens,
+    int32_t kv_tokens, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t q_local_offset,
+    int32_t kv_local_offset, int32_t storage_token_offset, int32_t causal_shift,
+    double softmax_scale, int32_t flags, int32_t dtype, int32_t quant_group_tokens, void* stream) {
+  sa::clear_error();
+  return sa::launch_update_int8(q, k, v, k_scales, v_scales, running_max, running_sum, accumulator,
+                                stride_qt, stride_qh, stride_kt, stride_kh, stride_vt, stride_vh,
+                                stride_ksg, stride_ksh, stride_vsg, stride_vsh, stride_st, stride_sh,
+                                stride_at, stride_ah, q_tokens, kv_tokens, q_heads, kv_heads,
+                                head_dim, q_local_offset, kv_local_offset, storage_token_offset,
+                                causal_shift, softmax_scale, flags, dtype, quant_group_tokens,
+                                static_cast<hipStream_t>(stream));
 }
 
 int32_t sa_finalize_attention(const float* accumulator, const float* running_max,

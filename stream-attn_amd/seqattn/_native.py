@@ -51,6 +51,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         + [c_int32] * 8
         + [c_double, c_int32, c_int32, c_void_p],
     ),
+    "sa_update_attention_state_int8": (
+        c_int32,
+        [c_void_p] * 8
+        + [c_int64] * 14
+        + [c_int32] * 9
+        + [c_double, c_int32, c_int32, c_int32, c_void_p],
+    ),
     "sa_finalize_attention": (
         c_int32,
         [c_void_p] * 5 + [c_int64] * 8 + [c_int32] * 4 + [c_void_p],

@@ -10,6 +10,7 @@ from .streaming import (
     hip_is_available,
     triton_is_available,
     update_attention_state,
+    update_attention_state_int8,
 )
 
 __all__ = [
@@ -17,4 +18,5 @@ __all__ = [
     "hip_is_available",
     "triton_is_available",
     "update_attention_state",
+    "update_attention_state_int8",
 ]

@@ -5,8 +5,10 @@ the reference wrappers (src/seqattn_core/kernels/streaming.py:205-271 and
 :345-371) and launch asynchronously on torch's current stream.  The launch
 parameters block_m/block_n/num_warps/num_stages are accepted for
 compatibility; the gfx950 kernel uses its own fixed tile (256 queries x 64
-keys per workgroup for head_dim <= 128).  ``finalize_attention`` gains optional ``running_max`` /
-``lse`` arguments that write the natural-log LSE ``[heads, tokens]``.
+keys per workgroup for head_dim <= 128).  ``update_attention_state_int8``
+(reference :274-342) dequantizes INT8 K/V inside the kernel.
+``finalize_attention`` gains optional ``running_max`` / ``lse`` arguments
+that write the natural-log LSE ``[heads, tokens]``.
 """
 
 from __future__ import annotations
@@ -82,6 +84,78 @@ def update_attention_state(
     _native.check(status, "sa_update_attention_state")
 
 
+def update_attention_state_int8(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    k_scales: torch.Tensor,
+    v_scales: torch.Tensor,
+    running_max: torch.Tensor,
+    running_sum: torch.Tensor,
+    accumulator: torch.Tensor,
+    *,
+    q_tokens: int,
+    kv_tokens: int,
+    q_local_offset: int,
+    kv_local_offset: int,
+    storage_token_offset: int,
+    causal_shift: int,
+    softmax_scale: float,
+    causal: bool,
+    initialize: bool,
+    block_m: int | None = None,
+    block_n: int | None = None,
+    num_warps: int | None = None,
+    num_stages: int | None = None,
+    quant_group_tokens: int = 64,
+) -> None:
+    """The chunk update with INT8 K/V (reference kernels/streaming.py:274-342).
+
+    Key ``j`` of K/V head ``h`` is dequantized as
+    ``q.dtype(float(k[j, h]) * float(k_scales[(storage_token_offset + j) //
+    quant_group_tokens, h]))`` inside the kernel (same for V), so the result
+    equals :func:`update_attention_state` on the dequantized K/V.
+    """
+    del block_m, block_n, num_warps, num_stages
+    _require_device(q, k, v, accumulator)
+    if k.dtype != torch.int8 or v.dtype != torch.int8:
+        raise ValueError("quantized K/V buffers must use int8")
+    if k_scales.dtype != torch.float16 or v_scales.dtype != torch.float16:
+        raise ValueError("quantized K/V scales must use float16")
+    if k_scales.device != q.device or v_scales.device != q.device:
+        raise ValueError("quantized K/V scales must live on the query device")
+    if k_scales.ndim != 2 or v_scales.ndim != 2:
+        raise ValueError("quantized K/V scales must use [groups, kv_heads] layout")
+    if running_max.stride() != running_sum.stride():
+        raise ValueError("running_max and running_sum must share strides")
+    if q_tokens > q.shape[0] or kv_tokens > k.shape[0] or kv_tokens > v.shape[0]:
+        raise ValueError("q_tokens/kv_tokens exceed the operand buffers")
+    if k.shape[1:] != v.shape[1:] or q.shape[2] != k.shape[2]:
+        raise ValueError("q, k and v head_dim / kv_heads must agree")
+    groups = (storage_token_offset + kv_tokens + quant_group_tokens - 1) // quant_group_tokens if kv_tokens else 0
+    for scales in (k_scales, v_scales):
+        if scales.shape[0] < groups or scales.shape[1] != k.shape[1]:
+            raise ValueError("scale buffers do not cover the quantized K/V tokens")
+    if accumulator.dtype != torch.float32 or running_max.dtype != torch.float32:
+        raise ValueError("the attention state must be float32")
+    flags = (_native.SA_FLAG_CAUSAL if causal else 0) | (
+        _native.SA_FLAG_INITIALIZE if initialize else 0
+    )
+    stream = torch.cuda.current_stream(q.device).cuda_stream
+    status = _native.lib().sa_update_attention_state_int8(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), k_scales.data_ptr(), v_scales.data_ptr(),
+        running_max.data_ptr(), running_sum.data_ptr(), accumulator.data_ptr(),
+        q.stride(0), q.stride(1), k.stride(0), k.stride(1), v.stride(0), v.stride(1),
+        k_scales.stride(0), k_scales.stride(1), v_scales.stride(0), v_scales.stride(1),
+        running_max.stride(0), running_max.stride(1),
+        accumulator.stride(0), accumulator.stride(1),
+        q_tokens, kv_tokens, q.shape[1], k.shape[1], q.shape[2],
+        q_local_offset, kv_local_offset, storage_token_offset, causal_shift,
+        float(softmax_scale), flags, _native.dtype_code(q.dtype), int(quant_group_tokens), stream,
+    )
+    _native.check(status, "sa_update_attention_state_int8")
+
+
 def finalize_attention(
     accumulator: torch.Tensor,
     running_sum: torch.Tensor,
@@ -123,4 +197,5 @@ __all__ = [
     "hip_is_available",
     "triton_is_available",
     "update_attention_state",
+    "update_attention_state_int8",
 ]

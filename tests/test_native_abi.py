@@ -68,3 +68,20 @@ def test_backend_resolution_never_falls_back_to_cpu():
     if not torch.cuda.is_available():
         with pytest.raises(RuntimeError, match="not available"):
             resolve_backend("hip", torch.bfloat16, torch.device("cuda"), head_dim=64)
+
+
+@pytest.mark.skipif(not _native.library_is_built(), reason="native library not built")
+def test_int8_update_argument_errors_surface_without_a_gpu():
+    lib = _native.lib()
+
+    def call(head_dim, dtype=0, group=64, offset=0):
+        return lib.sa_update_attention_state_int8(
+            *([None] * 8), *([0] * 14), 4, 4, 4, 4, head_dim, 0, 0, offset, 0, 1.0, 0, dtype, group, None)
+
+    assert call(136) == -3 and b"multiple of 16" in lib.sa_last_error()
+    assert call(256) == -3  # head_dim 256 is not covered by the INT8 path
+    assert call(24) == -3
+    assert call(64, dtype=5) == -2
+    assert call(64, group=48) == -1 and b"power of two" in lib.sa_last_error()
+    assert call(64, offset=-1) == -1
+    assert call(64) == -1 and b"null pointer" in lib.sa_last_error()
