@@ -269,6 +269,38 @@ int32_t sa_pipeline_stream_kv_gather(sa_pipeline* pipeline, const void* const* k
                                      void* compute_stream, sa_pipeline_stats* stats);
 
 /*
+ * INT8 K/V pages (PagedAttentionConfig.kv_storage_dtype == "int8"): give the
+ * pipeline one fp16 scale buffer per ring slot for K and for V, each holding
+ * kv_chunk_tokens * kv_heads values (row-major [row, kv_head]).  num_slots
+ * must equal the ring size; head_dim must be a multiple of 16 up to 128.
+ * No counterpart in the reference, whose paged workspace allocates per-slot
+ * group-scale tensors itself (paged/runtime/staging.py:97-107).
+ */
+int32_t sa_pipeline_attach_int8_scales(sa_pipeline* pipeline, void* const* k_scale_slots,
+                                       void* const* v_scale_slots, int32_t num_slots);
+
+/*
+ * sa_pipeline_stream_kv_gather for INT8 pages: fragment i holds
+ * fragment_tokens[i] int8 rows of kv_heads * head_dim bytes (K and V) and one
+ * fp16 scale per (row, K/V head) (k_scale_fragments[i], v_scale_fragments[i],
+ * kv_heads values per row).  Rows and scales are gathered into a ring slot
+ * and its scale slots and each slot is one INT8 update launch that
+ * dequantizes in the kernel, as update_attention_state_int8 does for a page
+ * (reference paged/runtime/triton.py:139-200).  Requires
+ * sa_pipeline_attach_int8_scales.
+ */
+int32_t sa_pipeline_stream_kv_gather_int8(sa_pipeline* pipeline, const void* const* k_fragments,
+                                          const void* const* v_fragments,
+                                          const void* const* k_scale_fragments,
+                                          const void* const* v_scale_fragments,
+                                          const int32_t* fragment_tokens, int32_t num_fragments,
+                                          int32_t kv_local_offset, int32_t* initialize,
+                                          int32_t q_tokens, int32_t q_local_offset,
+                                          int32_t causal_shift, double softmax_scale,
+                                          int32_t causal, void* compute_stream,
+                                          sa_pipeline_stats* stats);
+
+/*
  * HBM-resident execution: Q/K/V and out are device tensors (strides in
  * elements, unit stride over head_dim), so nothing crosses PCIe.  Same Q
  * super-block / K/V chunk decomposition as sa_pipeline_run, using the

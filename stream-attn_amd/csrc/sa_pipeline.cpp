@@ -59,6 +59,10 @@ struct sa_pipeline {
   void* k_slots[3] = {nullptr, nullptr, nullptr};
   void* v_slots[3] = {nullptr, nullptr, nullptr};
   int num_kv = 0;
+  // INT8 K/V: per ring slot, one fp16 scale per (row, K/V head) for K and V.
+  void* ks_slots[3] = {nullptr, nullptr, nullptr};
+  void* vs_slots[3] = {nullptr, nullptr, nullptr};
+  bool has_scales = false;
   float* m = nullptr;
   float* l = nullptr;
   float* acc = nullptr;
@@ -161,6 +165,33 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
   return 0;
 }
 
+// The INT8 K/V update over ring slot `slot` (int8 rows, per-row scales),
+// optionally bracketed by timing events.
+int32_t launch_timed_int8(sa_pipeline* p, int slot, int32_t q_tokens, int32_t kv_tokens,
+                          int32_t q_local_offset, int32_t kv_local_offset, int32_t causal_shift,
+                          double scale, int32_t flags, hipStream_t compute) {
+  if (p->timing) {
+    if (p->t_used == p->t_start.size()) {
+      hipEvent_t a = nullptr, b = nullptr;
+      SA_HIP_RETURN(hipEventCreate(&a));
+      SA_HIP_RETURN(hipEventCreate(&b));
+      p->t_start.push_back(a);
+      p->t_stop.push_back(b);
+    }
+    SA_HIP_RETURN(hipEventRecord(p->t_start[p->t_used], compute));
+  }
+  const int64_t qt = (int64_t)p->q_heads * p->head_dim;
+  const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+  int32_t rc = sa::launch_update_int8(
+      p->q_buffer, p->k_slots[slot], p->v_slots[slot], p->ks_slots[slot], p->vs_slots[slot], p->m,
+      p->l, p->acc, qt, p->head_dim, kt, p->head_dim, kt, p->head_dim, p->kv_heads, 1, p->kv_heads, 1,
+      p->q_heads, 1, qt, p->head_dim, q_tokens, kv_tokens, p->q_heads, p->kv_heads, p->head_dim,
+      q_local_offset, kv_local_offset, 0, causal_shift, scale, flags, p->dtype, 1, compute);
+  if (rc != 0) return rc;
+  if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
+  return 0;
+}
+
 // Where the K/V rows of a span live: pinned host rows copied through the ring
 // (tensor and paged modes), or device rows read in place (HBM-resident mode).
 struct KVSource {
@@ -229,14 +260,26 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
 // Ring slots are filled fragment piece by fragment piece (one hipMemcpyAsync
 // per piece and tensor), so page-sized host records feed chunk-sized kernel
 // launches without a host-side copy.
+//
+// INT8 mode (ks_frags / vs_frags non-null): fragments hold int8 rows of
+// kv_heads * head_dim bytes plus one fp16 scale per (row, K/V head); both are
+// gathered into the ring slot and its scale slot, and the launch dequantizes
+// in the kernel.
 int32_t apply_gather(sa_pipeline* p, const void* const* k_frags, const void* const* v_frags,
+                     const void* const* ks_frags, const void* const* vs_frags,
                      const int32_t* frag_tokens, int32_t nfrag, int32_t kv_local_offset,
                      bool* initialize, int32_t q_tokens, int32_t q_local_offset,
                      int32_t causal_shift, double scale, int32_t causal, hipStream_t compute,
                      sa_pipeline_stats* st) {
+  const bool int8 = ks_frags != nullptr;
+  if (int8 && (!vs_frags || !p->has_scales)) {
+    sa::set_error("INT8 K/V gather needs scale fragments and a pipeline with scale slots");
+    return SA_ERR_BAD_STATE;
+  }
   int64_t total = 0;
   for (int32_t i = 0; i < nfrag; ++i) {
-    if (frag_tokens[i] < 0 || (frag_tokens[i] > 0 && (!k_frags[i] || !v_frags[i]))) {
+    if (frag_tokens[i] < 0 || (frag_tokens[i] > 0 && (!k_frags[i] || !v_frags[i])) ||
+        (int8 && frag_tokens[i] > 0 && (!ks_frags[i] || !vs_frags[i]))) {
       sa::set_error("bad K/V fragment %d (%d tokens)", i, frag_tokens[i]);
       return SA_ERR_INVALID_ARGUMENT;
     }
@@ -251,6 +294,8 @@ int32_t apply_gather(sa_pipeline* p, const void* const* k_frags, const void* con
   if (causal) visible_end = std::max<int64_t>(0, (int64_t)q_local_offset + q_tokens + causal_shift);
   const int64_t qt = (int64_t)p->q_heads * p->head_dim;
   const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+  const int64_t row_bytes = int8 ? kt : p->kv_row_bytes;
+  const int64_t scale_row_bytes = (int64_t)p->kv_heads * 2;
   int32_t frag = 0;       // fragment holding the next row
   int64_t frag_row = 0;   // rows of that fragment already consumed
   for (int64_t start = 0; start < total; start += p->kv_chunk) {
@@ -268,24 +313,36 @@ int32_t apply_gather(sa_pipeline* p, const void* const* k_frags, const void* con
         frag_row = 0;
       }
       const int64_t rows = std::min<int64_t>(n - filled, frag_tokens[frag] - frag_row);
-      const int64_t bytes = rows * p->kv_row_bytes;
-      const int64_t src_off = frag_row * p->kv_row_bytes;
-      SA_HIP_RETURN(hipMemcpyAsync(kd + filled * p->kv_row_bytes,
+      const int64_t bytes = rows * row_bytes;
+      const int64_t src_off = frag_row * row_bytes;
+      SA_HIP_RETURN(hipMemcpyAsync(kd + filled * row_bytes,
                                    static_cast<const char*>(k_frags[frag]) + src_off, bytes,
                                    hipMemcpyHostToDevice, p->h2d));
-      SA_HIP_RETURN(hipMemcpyAsync(vd + filled * p->kv_row_bytes,
+      SA_HIP_RETURN(hipMemcpyAsync(vd + filled * row_bytes,
                                    static_cast<const char*>(v_frags[frag]) + src_off, bytes,
                                    hipMemcpyHostToDevice, p->h2d));
+      if (int8) {
+        const int64_t sbytes = rows * scale_row_bytes;
+        const int64_t ssrc = frag_row * scale_row_bytes;
+        SA_HIP_RETURN(hipMemcpyAsync(static_cast<char*>(p->ks_slots[slot]) + filled * scale_row_bytes,
+                                     static_cast<const char*>(ks_frags[frag]) + ssrc, sbytes,
+                                     hipMemcpyHostToDevice, p->h2d));
+        SA_HIP_RETURN(hipMemcpyAsync(static_cast<char*>(p->vs_slots[slot]) + filled * scale_row_bytes,
+                                     static_cast<const char*>(vs_frags[frag]) + ssrc, sbytes,
+                                     hipMemcpyHostToDevice, p->h2d));
+      }
       filled += rows;
       frag_row += rows;
     }
     SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
-    add_stats(st, 2 * (int64_t)n * p->kv_row_bytes, 0, 0, 1, 0);
+    add_stats(st, 2 * (int64_t)n * (row_bytes + (int8 ? scale_row_bytes : 0)), 0, 0, 1, 0);
     SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
     const int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (*initialize ? SA_FLAG_INITIALIZE : 0);
-    int32_t rc = launch_timed(p, p->q_buffer, qt, p->head_dim, kd, kt, p->head_dim, vd, kt,
-                              p->head_dim, q_tokens, n, q_local_offset, (int32_t)position,
-                              causal_shift, scale, flags, compute);
+    int32_t rc = int8 ? launch_timed_int8(p, slot, q_tokens, n, q_local_offset, (int32_t)position,
+                                          causal_shift, scale, flags, compute)
+                      : launch_timed(p, p->q_buffer, qt, p->head_dim, kd, kt, p->head_dim, vd, kt,
+                                     p->head_dim, q_tokens, n, q_local_offset, (int32_t)position,
+                                     causal_shift, scale, flags, compute);
     if (rc != 0) return rc;
     SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
     p->kv_pending[slot] = true;
@@ -557,9 +614,63 @@ int32_t sa_pipeline_stream_kv_gather(sa_pipeline* p, const void* const* k_fragme
   sa::DeviceGuard guard(p->device);
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
   bool init = *initialize != 0;
-  int32_t rc = apply_gather(p, k_fragments, v_fragments, fragment_tokens, num_fragments,
-                            kv_local_offset, &init, q_tokens, q_local_offset, causal_shift,
-                            softmax_scale, causal, compute, stats);
+  int32_t rc = apply_gather(p, k_fragments, v_fragments, nullptr, nullptr, fragment_tokens,
+                            num_fragments, kv_local_offset, &init, q_tokens, q_local_offset,
+                            causal_shift, softmax_scale, causal, compute, stats);
+  *initialize = init ? 1 : 0;
+  return rc;
+}
+
+int32_t sa_pipeline_attach_int8_scales(sa_pipeline* p, void* const* k_scale_slots,
+                                       void* const* v_scale_slots, int32_t num_slots) {
+  sa::clear_error();
+  if (!p || !k_scale_slots || !v_scale_slots || num_slots != p->num_kv) {
+    sa::set_error("sa_pipeline_attach_int8_scales: need %d K and V scale slots",
+                  p ? p->num_kv : 0);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (p->head_dim % 16 != 0 || p->head_dim > 128) {
+    sa::set_error("sa_pipeline_attach_int8_scales: INT8 K/V needs head_dim a multiple of 16 up to "
+                  "128, got %d", p->head_dim);
+    return SA_ERR_UNSUPPORTED_HEAD_DIM;
+  }
+  for (int i = 0; i < num_slots; ++i) {
+    if (!k_scale_slots[i] || !v_scale_slots[i] ||
+        (reinterpret_cast<uintptr_t>(k_scale_slots[i]) | reinterpret_cast<uintptr_t>(v_scale_slots[i])) % 2) {
+      sa::set_error("sa_pipeline_attach_int8_scales: scale slot %d is null or misaligned", i);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+  }
+  for (int i = 0; i < num_slots; ++i) {
+    p->ks_slots[i] = k_scale_slots[i];
+    p->vs_slots[i] = v_scale_slots[i];
+  }
+  p->has_scales = true;
+  return 0;
+}
+
+int32_t sa_pipeline_stream_kv_gather_int8(
+    sa_pipeline* p, const void* const* k_fragments, const void* const* v_fragments,
+    const void* const* k_scale_fragments, const void* const* v_scale_fragments,
+    const int32_t* fragment_tokens, int32_t num_fragments, int32_t kv_local_offset,
+    int32_t* initialize, int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift,
+    double softmax_scale, int32_t causal, void* compute_stream, sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p || !initialize || num_fragments < 0 ||
+      (num_fragments > 0 && (!k_fragments || !v_fragments || !k_scale_fragments ||
+                             !v_scale_fragments || !fragment_tokens))) {
+    sa::set_error("sa_pipeline_stream_kv_gather_int8: null argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa::DeviceGuard guard(p->device);
+  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  bool init = *initialize != 0;
+  static const void* const kNoFragment = nullptr;
+  int32_t rc = apply_gather(p, k_fragments, v_fragments,
+                            num_fragments > 0 ? k_scale_fragments : &kNoFragment,
+                            num_fragments > 0 ? v_scale_fragments : &kNoFragment, fragment_tokens,
+                            num_fragments, kv_local_offset, &init, q_tokens, q_local_offset,
+                            causal_shift, softmax_scale, causal, compute, stats);
   *initialize = init ? 1 : 0;
   return rc;
 }

@@ -94,6 +94,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_int32, ctypes.POINTER(c_int32), c_int32, c_int32, c_int32, c_double, c_int32, c_void_p,
          ctypes.POINTER(PipelineStats)],
     ),
+    "sa_pipeline_attach_int8_scales": (
+        c_int32,
+        [c_void_p, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p), c_int32],
+    ),
+    "sa_pipeline_stream_kv_gather_int8": (
+        c_int32,
+        [c_void_p, ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p), ctypes.POINTER(c_void_p),
+         ctypes.POINTER(c_void_p), ctypes.POINTER(c_int32), c_int32, c_int32, ctypes.POINTER(c_int32),
+         c_int32, c_int32, c_int32, c_double, c_int32, c_void_p, ctypes.POINTER(PipelineStats)],
+    ),
     "sa_pipeline_run_resident": (
         c_int32,
         [c_void_p] * 6 + [c_int64] * 9

@@ -11,7 +11,10 @@ rows at the record's ``v_offset``, INT8 scales after them) in page-locked
 memory, so a hit is served by the copy engine straight from the slot and a
 miss from an aligned store is read into its slot as one whole record (the
 reference copies between an mmap region and a staging tensor on every hit and
-insert).  Slots referenced by copies still in flight are never evicted.
+insert).  Slots referenced by copies still in flight are never evicted.  For
+INT8 pages a slot also holds the group scales expanded to one scale per
+(row, head) for K and for V (``token_scale_layout``), the form the GPU
+gather copies next to the rows.
 """
 
 from __future__ import annotations
@@ -28,6 +31,28 @@ from ..storage.records import kv_record_pages
 from .layout import KVLayout, PageDescriptor
 from .memory_budget import HostMemoryPlan
 from .slab import PinnedSlab
+
+
+def token_scale_layout(record: PageDescriptor, layout: KVLayout) -> tuple[int, int, int]:
+    """Slot offsets of the per-row K and V scales of an INT8 record, and the
+    slot bytes it needs; (0, 0, record bytes) for other storage dtypes."""
+    if layout.storage_dtype != "int8":
+        return 0, 0, record.storage_bytes
+    per_tensor = record.padded_tokens * layout.heads * 2
+    k_offset = -(-record.storage_bytes // 256) * 256
+    return k_offset, k_offset + per_tensor, k_offset + 2 * per_tensor
+
+
+def expand_token_scales(raw: torch.Tensor, record: PageDescriptor, layout: KVLayout) -> None:
+    """Fill the per-row scale areas of an INT8 slot image ``raw`` (uint8)
+    from its ``[groups, heads]`` group scales: row j gets group j // quant_group_tokens."""
+    k_offset, v_offset, _ = token_scale_layout(record, layout)
+    rows, heads, group = record.padded_tokens, layout.heads, layout.quant_group_tokens
+    groups = record.scale_bytes // (2 * heads)
+    for scale_offset, token_offset in ((record.k_scale_offset, k_offset), (record.v_scale_offset, v_offset)):
+        grouped = raw[scale_offset : scale_offset + record.scale_bytes].view(torch.float16).view(groups, heads)
+        per_row = raw[token_offset : token_offset + rows * heads * 2].view(torch.float16).view(rows, heads)
+        per_row.copy_(grouped.repeat_interleave(group, dim=0)[:rows])
 
 
 @dataclass(frozen=True)
@@ -51,7 +76,7 @@ class KVPageCache:
     ) -> None:
         self.layout = layout
         self.records = {r.page_id: r for r in kv_record_pages(pages, layout)}
-        slot_bytes = max((r.storage_bytes for r in self.records.values()), default=0)
+        slot_bytes = max((token_scale_layout(r, layout)[2] for r in self.records.values()), default=0)
         count = min(len(pages), capacity_bytes // slot_bytes) if slot_bytes else 0
         self.memory_plan = memory_plan
         self.registered_bytes = 0
@@ -154,6 +179,7 @@ class KVPageCache:
             groups = math.ceil(n / self.layout.quant_group_tokens)
             ksd[:groups].copy_(k_scales[:groups])
             vsd[:groups].copy_(v_scales[:groups])
+            expand_token_scales(self.slab.bytes(slot), self.records[page.page_id], self.layout)
         self.commit(page, slot)
         return True
 
@@ -238,4 +264,4 @@ class KVPageCache:
         self.close()
 
 
-__all__ = ["CacheLookup", "KVPageCache"]
+__all__ = ["CacheLookup", "KVPageCache", "expand_token_scales", "token_scale_layout"]

@@ -19,7 +19,10 @@ Same entry point, arguments, validation and stats as the reference's
 * K/V pages that the bottom-right causal mask hides from a whole Q block are
   neither read nor copied;
 * ``run_with_device_output`` keeps the output in HBM (device-consumer mode,
-  an extension: the reference requires host output for paged runs).
+  an extension: the reference requires host output for paged runs);
+* INT8 pages cross PCIe as int8 rows plus one fp16 scale per (row, head) and
+  are dequantized inside the update kernel, exactly as the reference's
+  ``update_attention_state_int8`` does per page.
 
 Host memory is accounted in a ``HostMemoryPlan`` with the reference's
 categories; the page-locked cache slots are charged to ``cache``, staging
@@ -46,14 +49,14 @@ from ..stats import PagedAttentionStats
 from ..storage.records import kv_record_pages
 from ..streaming.backend import resolve_backend
 from ..streaming.workspace import CudaWorkspace
-from .cache import KVPageCache
+from .cache import KVPageCache, expand_token_scales, token_scale_layout
 from .layout import KVLayout, PageDescriptor, PageReadMetrics, TensorLayout, pages_by_segment, validate_cu_seqlens
 from .memory_budget import HostMemoryPlan, HostMemorySnapshot
 from .protocols import PageSink, PageSource
 from .schedule import Fragment, FragmentQueue, QGroup, plan_q_groups
 from .slab import PinnedSlab
 
-_EXACT_STORAGE = {"bf16", "fp16"}
+_NATIVE_STORAGE = {"bf16", "fp16", "int8"}
 
 
 def _backing_is_nvme(obj: object) -> bool:
@@ -118,15 +121,17 @@ class _StageRing:
 class _Load:
     """One K/V page on its way into page-locked memory."""
 
-    __slots__ = ("page", "future", "k_address", "v_address", "owner", "commit_slot")
+    __slots__ = ("page", "future", "k_address", "v_address", "owner", "commit_slot", "ks_address", "vs_address")
 
-    def __init__(self, page, future, k_address, v_address, owner, commit_slot=None):
+    def __init__(self, page, future, k_address, v_address, owner, commit_slot=None, ks_address=0, vs_address=0):
         self.page = page
         self.future = future
         self.k_address = k_address
         self.v_address = v_address
         self.owner = owner
         self.commit_slot = commit_slot
+        self.ks_address = ks_address
+        self.vs_address = vs_address
 
 
 class PagedAttentionRunner:
@@ -241,10 +246,11 @@ class PagedAttentionRunner:
         self._nvtx = bool(config.attention.enable_nvtx and torch.cuda.is_available())
         q_layout, kv_layout, q_bounds, k_bounds = validate_source_contract(
             q_source, kv_source, cu_seqlens_q, cu_seqlens_k, config)
-        if kv_layout.storage_dtype not in _EXACT_STORAGE:
-            if kv_layout.storage_dtype == "fp32":
-                raise ValueError("the HIP paged backend does not support FP32 K/V storage")
-            raise ValueError("the HIP paged backend supports bf16/fp16 K/V storage; INT8 pages are not supported")
+        if kv_layout.storage_dtype not in _NATIVE_STORAGE:
+            raise ValueError("the HIP paged backend supports bf16, fp16 and int8 K/V storage, not "
+                             f"{kv_layout.storage_dtype}")
+        if kv_layout.storage_dtype == "int8" and (q_layout.head_dim % 16 or q_layout.head_dim > 128):
+            raise ValueError("INT8 K/V pages need head_dim a multiple of 16 and at most 128")
         attention = config.attention
         if device_mode:
             attention = replace(attention, output_mode="device_consumer")
@@ -388,7 +394,8 @@ class PagedAttentionRunner:
             pages = [p for p in kv_pages if p.segment_token_start < visible_end] or list(kv_pages[:1])
         else:
             pages = list(kv_pages)
-        queue = FragmentQueue(kv_row_bytes)
+        int8 = state.int8
+        queue = FragmentQueue(kv_row_bytes, state.scale_row_bytes if int8 else 0)
         initialize = ctypes.c_int32(1)
         issued = 0
         kv_chunk = plan.kv_chunk_tokens
@@ -401,11 +408,20 @@ class PagedAttentionRunner:
             v_ptrs = (ctypes.c_void_p * count)(*[p[1] for p in pieces])
             lengths = (ctypes.c_int32 * count)(*[p[2] for p in pieces])
             copy_started = time.perf_counter()
-            _native.check(
-                lib.sa_pipeline_stream_kv_gather(
-                    handle, k_ptrs, v_ptrs, lengths, count, issued, ctypes.byref(initialize), q_tokens,
-                    q_local_offset, shift, float(scale), int(bool(causal)), compute_ptr, native_ref),
-                "sa_pipeline_stream_kv_gather")
+            if int8:
+                ks_ptrs = (ctypes.c_void_p * count)(*[p[3] for p in pieces])
+                vs_ptrs = (ctypes.c_void_p * count)(*[p[4] for p in pieces])
+                _native.check(
+                    lib.sa_pipeline_stream_kv_gather_int8(
+                        handle, k_ptrs, v_ptrs, ks_ptrs, vs_ptrs, lengths, count, issued, ctypes.byref(initialize),
+                        q_tokens, q_local_offset, shift, float(scale), int(bool(causal)), compute_ptr, native_ref),
+                    "sa_pipeline_stream_kv_gather_int8")
+            else:
+                _native.check(
+                    lib.sa_pipeline_stream_kv_gather(
+                        handle, k_ptrs, v_ptrs, lengths, count, issued, ctypes.byref(initialize), q_tokens,
+                        q_local_offset, shift, float(scale), int(bool(causal)), compute_ptr, native_ref),
+                    "sa_pipeline_stream_kv_gather")
             stats.pinned_copy_seconds += time.perf_counter() - copy_started
             event = torch.cuda.Event()
             event.record(state.workspace.h2d_stream)
@@ -429,7 +445,8 @@ class PagedAttentionRunner:
                 self._account_read(stats, metrics, state.kv_is_nvme)
             if load.commit_slot is not None:
                 state.cache.commit(load.page, load.commit_slot)
-            queue.push(Fragment(load.k_address, load.v_address, load.page.valid_tokens, load.owner))
+            queue.push(Fragment(load.k_address, load.v_address, load.page.valid_tokens, load.owner,
+                                load.ks_address, load.vs_address))
             stats.kv_pages += 1
             if queue.rows >= kv_chunk:
                 issue((queue.rows // kv_chunk) * kv_chunk)
@@ -506,10 +523,17 @@ class _RunState:
         self.q_is_nvme = False
         self.out_is_nvme = False
         self.q_rows = 0
+        self.int8 = False
+        self.kv_layout = None
+        self.scale_row_bytes = 0
+        self.scale_ring: list[torch.Tensor] = []
 
     def open(self, runner, q_source, kv_source, sink, memory_plan, config, q_layout, kv_layout, plan, q_bounds,
              device_mode, device):
         self.memory_plan = memory_plan
+        self.kv_layout = kv_layout
+        self.int8 = kv_layout.storage_dtype == "int8"
+        self.scale_row_bytes = kv_layout.heads * 2
         self.kv_is_nvme = _backing_is_nvme(kv_source)
         self.q_is_nvme = _backing_is_nvme(q_source)
         self.out_is_nvme = sink is not None and _backing_is_nvme(sink)
@@ -542,7 +566,7 @@ class _RunState:
 
         # Page-locked staging: K/V stage slots, the Q block, host output slots.
         records = kv_record_pages(kv_source.kv_pages, kv_layout)
-        record_bytes = max((r.storage_bytes for r in records), default=4096)
+        record_bytes = max((token_scale_layout(r, kv_layout)[2] for r in records), default=4096)
         min_page = min((p.valid_tokens for p in kv_source.kv_pages), default=1)
         stage_count = 0
         if self.zero_copy_kv is None:
@@ -588,6 +612,17 @@ class _RunState:
         run_plan = replace(plan, q_chunk_tokens=q_rows) if q_rows < plan.q_chunk_tokens else plan
         with torch.cuda.device(device):
             self.workspace = CudaWorkspace(run_plan)
+            if self.int8:
+                # One fp16 scale per (row, K/V head) per ring slot, for K and for V.
+                shape = (run_plan.kv_chunk_tokens, run_plan.kv_heads)
+                ks = [torch.empty(shape, dtype=torch.float16, device=device) for _ in self.workspace.k]
+                vs = [torch.empty(shape, dtype=torch.float16, device=device) for _ in self.workspace.k]
+                self.scale_ring = ks + vs
+                count = len(ks)
+                _native.check(_native.lib().sa_pipeline_attach_int8_scales(
+                    self.workspace.handle, (ctypes.c_void_p * count)(*[t.data_ptr() for t in ks]),
+                    (ctypes.c_void_p * count)(*[t.data_ptr() for t in vs]), count),
+                    "sa_pipeline_attach_int8_scales")
         self.q_event = torch.cuda.Event()
         self.q_event_pending = False
 
@@ -601,18 +636,21 @@ class _RunState:
         slot, lookup = self.cache.lookup(page)
         stats.cache_lookup_seconds += lookup.seconds
         record = self.cache.record(page) if self.cache.records else None
+        ks_offset, vs_offset, _ = token_scale_layout(record, self.kv_layout)
         if slot is not None:
             slab = self.cache.slab
             slab.hold(slot)
             base = slab.address(slot)
-            return _Load(page, None, base, base + record.v_offset, ("cache", slot))
+            return _Load(page, None, base, base + record.v_offset, ("cache", slot),
+                         ks_address=base + ks_offset, vs_address=base + vs_offset)
         slot = self.cache.reserve(page)
         if slot is not None:
             slab = self.cache.slab
             slab.hold(slot)
             future = self.pool.submit(self._read_kv_into, slab, slot, page, record)
             base = slab.address(slot)
-            return _Load(page, future, base, base + record.v_offset, ("cache", slot), commit_slot=slot)
+            return _Load(page, future, base, base + record.v_offset, ("cache", slot), commit_slot=slot,
+                         ks_address=base + ks_offset, vs_address=base + vs_offset)
         # Uncached: a staging slot (flush queued rows if every slot is referenced).
         stages = self.stages
         while not stages.free:
@@ -624,19 +662,32 @@ class _RunState:
         stages.slab.hold(stage)
         future = self.pool.submit(self._read_kv_into, stages.slab, stage, page, record)
         base = stages.slab.address(stage)
-        return _Load(page, future, base, base + record.v_offset, ("stage", stage))
+        return _Load(page, future, base, base + record.v_offset, ("stage", stage),
+                     ks_address=base + ks_offset, vs_address=base + vs_offset)
 
     def _read_kv_into(self, slab: PinnedSlab, slot: int, page: PageDescriptor, record: PageDescriptor):
+        """Read the page's record image into ``slot`` (I/O worker thread); INT8
+        records then get their per-row scales."""
         destination = slab.bytes(slot)
         reader = self.kv_reader
+        layout = self.kv_layout
         if hasattr(reader, "read_kv_record"):
-            return reader.read_kv_record(page, destination)
-        layout = self.cache.layout
-        dtype = layout.storage_torch_dtype
-        shape = (record.padded_tokens, layout.heads, layout.head_dim)
-        k_view = destination[: record.k_bytes].view(dtype).view(shape)
-        v_view = destination[record.v_offset : record.v_offset + record.v_bytes].view(dtype).view(shape)
-        return reader.read_kv(page, k_view, v_view)
+            metrics = reader.read_kv_record(page, destination)
+        else:
+            dtype = layout.storage_torch_dtype
+            shape = (record.padded_tokens, layout.heads, layout.head_dim)
+            k_view = destination[: record.k_bytes].view(dtype).view(shape)
+            v_view = destination[record.v_offset : record.v_offset + record.v_bytes].view(dtype).view(shape)
+            scales = ()
+            if self.int8:
+                groups = record.scale_bytes // (2 * layout.heads)
+                scales = tuple(
+                    destination[offset : offset + record.scale_bytes].view(torch.float16).view(groups, layout.heads)
+                    for offset in (record.k_scale_offset, record.v_scale_offset))
+            metrics = reader.read_kv(page, k_view, v_view, *scales)
+        if self.int8:
+            expand_token_scales(destination, record, layout)
+        return metrics
 
     def release(self, owner, event) -> None:
         if owner is None:
@@ -754,6 +805,7 @@ class _RunState:
             self.stages.slab.close()
         self.q_stage = None
         self.out_stage = []
+        self.scale_ring = []
         if self.pinned_registered:
             self.memory_plan.release("pinned", self.pinned_registered)
             self.pinned_registered = 0

@@ -94,12 +94,15 @@ def plan_q_groups(pages: Sequence[PageDescriptor], block_rows: int) -> list[QGro
 @dataclass
 class Fragment:
     """Contiguous host rows of K and V (addresses) plus the owner released
-    once the rows have been copied."""
+    once the rows have been copied; INT8 pages also carry per-row K and V
+    scale addresses."""
 
     k_address: int
     v_address: int
     rows: int
     owner: object = None
+    ks_address: int = 0
+    vs_address: int = 0
 
 
 @dataclass
@@ -107,6 +110,7 @@ class FragmentQueue:
     """K/V rows waiting for their H2D copy, in segment order."""
 
     row_bytes: int
+    scale_row_bytes: int = 0
     fragments: deque = field(default_factory=deque)
     rows: int = 0
 
@@ -115,18 +119,18 @@ class FragmentQueue:
             self.fragments.append(fragment)
             self.rows += fragment.rows
 
-    def take(self, rows: int) -> tuple[list[tuple[int, int, int]], list[object]]:
-        """Remove the first ``rows`` rows: returns (k, v, rows) pieces and the
-        owners whose rows have now all been taken."""
+    def take(self, rows: int) -> tuple[list[tuple[int, int, int, int, int]], list[object]]:
+        """Remove the first ``rows`` rows: returns (k, v, rows, k_scales,
+        v_scales) pieces and the owners whose rows have now all been taken."""
         if rows > self.rows:
             raise ValueError("not enough queued rows")
-        pieces: list[tuple[int, int, int]] = []
+        pieces: list[tuple[int, int, int, int, int]] = []
         finished: list[object] = []
         left = rows
         while left:
             head = self.fragments[0]
             n = min(left, head.rows)
-            pieces.append((head.k_address, head.v_address, n))
+            pieces.append((head.k_address, head.v_address, n, head.ks_address, head.vs_address))
             if n == head.rows:
                 self.fragments.popleft()
                 finished.append(head.owner)
@@ -134,6 +138,9 @@ class FragmentQueue:
                 step = n * self.row_bytes
                 head.k_address += step
                 head.v_address += step
+                if self.scale_row_bytes:
+                    head.ks_address += n * self.scale_row_bytes
+                    head.vs_address += n * self.scale_row_bytes
                 head.rows -= n
             left -= n
         self.rows -= rows

@@ -246,12 +246,50 @@ def test_fragment_queue_splits_pages_across_chunks():
     queue.push(Fragment(1000, 5000, 6, "a"))
     queue.push(Fragment(2000, 6000, 4, "b"))
     pieces, done = queue.take(8)
-    assert pieces == [(1000, 5000, 6), (2000, 6000, 2)] and done == ["a"]
+    assert pieces == [(1000, 5000, 6, 0, 0), (2000, 6000, 2, 0, 0)] and done == ["a"]
     pieces, done = queue.take(2)
-    assert pieces == [(2020, 6020, 2)] and done == ["b"]
+    assert pieces == [(2020, 6020, 2, 0, 0)] and done == ["b"]
     assert queue.rows == 0
     with pytest.raises(ValueError):
         queue.take(1)
+
+
+def test_fragment_queue_advances_int8_scale_rows():
+    queue = FragmentQueue(row_bytes=64, scale_row_bytes=4)
+    queue.push(Fragment(1000, 5000, 6, "a", ks_address=9000, vs_address=9500))
+    queue.push(Fragment(2000, 6000, 4, "b", ks_address=8000, vs_address=8500))
+    pieces, done = queue.take(3)
+    assert pieces == [(1000, 5000, 3, 9000, 9500)] and done == []
+    pieces, done = queue.take(5)
+    assert pieces == [(1192, 5192, 3, 9012, 9512), (2000, 6000, 2, 8000, 8500)] and done == ["a"]
+    pieces, _ = queue.take(2)
+    assert pieces == [(2128, 6128, 2, 8008, 8508)]
+
+
+def test_int8_slots_carry_per_row_scales():
+    from seqattn.paged.cache import expand_token_scales, token_scale_layout
+    from seqattn.paged.layout import KVLayout, PageDescriptor
+    from seqattn.storage.records import kv_record_pages
+
+    layout = KVLayout(total_tokens=150, heads=3, head_dim=32, source_dtype="bf16", storage_dtype="int8")
+    page = PageDescriptor(page_id=0, segment_id=0, token_start=0, segment_token_start=0, valid_tokens=150,
+                          padded_tokens=160)
+    record = kv_record_pages([page], layout)[0]
+    k_offset, v_offset, end = token_scale_layout(record, layout)
+    assert k_offset >= record.storage_bytes and k_offset % 256 == 0
+    assert v_offset == k_offset + 160 * 3 * 2 and end == v_offset + 160 * 3 * 2
+    raw = torch.zeros(end, dtype=torch.uint8)
+    groups = torch.arange(3 * 3, dtype=torch.float16).view(3, 3)  # ceil(160 / 64) groups
+    raw[record.k_scale_offset : record.k_scale_offset + record.scale_bytes].view(torch.float16).copy_(groups.flatten())
+    raw[record.v_scale_offset : record.v_scale_offset + record.scale_bytes].view(torch.float16).copy_(-groups.flatten())
+    expand_token_scales(raw, record, layout)
+    per_row_k = raw[k_offset:v_offset].view(torch.float16).view(160, 3)
+    per_row_v = raw[v_offset:end].view(torch.float16).view(160, 3)
+    for row in (0, 63, 64, 127, 128, 159):
+        assert torch.equal(per_row_k[row], groups[row // 64])
+        assert torch.equal(per_row_v[row], -groups[row // 64])
+    dense = token_scale_layout(record, KVLayout(150, 3, 32, "bf16", "bf16"))
+    assert dense == (0, 0, record.storage_bytes)
 
 
 def test_source_contract_errors():
