@@ -83,6 +83,9 @@ def parse_args():
                          "heads, peaked scores, 8 GiB workspace, with LSE; 65k: 65,536 tokens x 32 heads "
                          "resident in HBM and streamed with 1 GiB; projected: 61,312 tokens of hidden "
                          "size 5,376 through QKV projection, attention and output projection")
+    ap.add_argument("--kv-storage", default="bf16", choices=["bf16", "int8"],
+                    help="paged workload: K/V page storage dtype (int8: per-64-token-group scales, "
+                         "dequantized in the kernel)")
     ap.add_argument("--store-dir", type=Path, default=None,
                     help="paged: directory for the temporary page store (default: $TMPDIR)")
     ap.add_argument("--direct-io", default="auto", choices=["auto", "on", "off"],
@@ -801,7 +804,8 @@ def paged_main(args) -> int:
     outliers = torch.from_numpy(np.sort(gen.choice(n, n // 100, replace=False)))
     k[outliers] *= 8
     cu = torch.tensor([0, n], dtype=torch.int32)
-    page_bytes = PAGED_PAGE_TOKENS * h * d * 2
+    storage = args.kv_storage
+    page_bytes = PAGED_PAGE_TOKENS * h * d * (1 if storage == "int8" else 2)
     parent = args.store_dir or Path(os.environ.get("TMPDIR", tempfile.gettempdir()))
     parent.mkdir(parents=True, exist_ok=True)
     direct_io = args.direct_io != "off"
@@ -809,14 +813,14 @@ def paged_main(args) -> int:
         t0 = time.perf_counter()
         try:
             store = NvmeQKVWriter.from_tensors(root / "qkv", q, k, v, cu, cu, page_target_bytes=page_bytes,
-                                               block_n=64, direct_io=direct_io)
+                                               block_n=64, kv_storage_dtype=storage, direct_io=direct_io)
         except RuntimeError as error:
             if args.direct_io == "on":
                 raise
             log(f"paged: O_DIRECT unavailable ({error}); using buffered store I/O")
             direct_io = False
             store = NvmeQKVWriter.from_tensors(root / "qkv2", q, k, v, cu, cu, page_target_bytes=page_bytes,
-                                               block_n=64, direct_io=False)
+                                               block_n=64, kv_storage_dtype=storage, direct_io=False)
         log(f"paged: store written in {time.perf_counter() - t0:.1f}s ({len(store.kv_pages)} K/V pages, "
             f"direct_io={direct_io})")
         config = PagedAttentionConfig(
@@ -825,8 +829,10 @@ def paged_main(args) -> int:
             page_target_bytes=page_bytes,
             io_queue_depth=4,
             direct_io=direct_io,
+            kv_storage_dtype=storage,
         )
         runner = PagedAttentionRunner(config)
+        kv_pages = store.kv_pages
         out = torch.empty((n, h, d), dtype=torch.bfloat16, device="cuda")
         lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
         for i in range(args.warmup):
@@ -854,9 +860,24 @@ def paged_main(args) -> int:
         rows = np.unique(np.concatenate([[0, n // 4, n // 2, 3 * n // 4, n - 1],
                                          rng.choice(n, args.parity_rows // 4, replace=False)]))
         u16 = lambda t: t.view(torch.int16).numpy().view(np.uint16)  # noqa: E731
+        k_ref, v_ref = u16(k), u16(v)
+        unquantized = None
+        if storage == "int8":
+            from oracle.seqattn_oracle import dequantize_int8_groups, quantize_int8_groups
+
+            # The pages' K/V as stored: quantized per page, dequantized with the kernel's rounding.
+            k_ref, v_ref = k_ref.copy(), v_ref.copy()
+            for page in kv_pages:
+                span = slice(page.token_start, page.token_stop)
+                for array in (k_ref, v_ref):
+                    array[span] = dequantize_int8_groups(*quantize_int8_groups(array[span]))
+            with threadpool_limits(1):
+                unquantized, _ = chunked_attention(u16(q[rows]), u16(k), u16(v), [0, rows.size], [0, n],
+                                                   q_chunk_tokens=rows.size, kv_chunk_tokens=8192,
+                                                   workers=args.cpu_workers)
         t0 = time.perf_counter()
         with threadpool_limits(1):
-            ref_o, ref_l = chunked_attention(u16(q[rows]), u16(k), u16(v), [0, rows.size], [0, n],
+            ref_o, ref_l = chunked_attention(u16(q[rows]), k_ref, v_ref, [0, rows.size], [0, n],
                                              q_chunk_tokens=rows.size, kv_chunk_tokens=8192,
                                              workers=args.cpu_workers)
         cpu_s = time.perf_counter() - t0
@@ -870,7 +891,15 @@ def paged_main(args) -> int:
         parity = {"rows": int(rows.size), "heads": h, "max_abs_o": float(diff.max()), "rel_l2": rel_l2,
                   "max_scaled_err": scaled, "max_abs_lse": err_l,
                   "ok": bool(diff.max() <= 2e-2 and rel_l2 <= 5e-3 and scaled <= 2.0**-5 and err_l <= 1e-3),
-                  "reference": "CPU oracle (FP32 chunked online softmax)"}
+                  "reference": "CPU oracle (FP32 chunked online softmax)"
+                               + (" on the pages' dequantized K/V" if storage == "int8" else "")}
+        if unquantized is not None:
+            flat_got, flat_ref = got.reshape(-1), unquantized.reshape(-1)
+            parity["vs_unquantized_rel_l2"] = float(np.linalg.norm(flat_got - flat_ref) / np.linalg.norm(flat_ref))
+            parity["vs_unquantized_cosine"] = float(
+                np.dot(flat_got, flat_ref) / (np.linalg.norm(flat_got) * np.linalg.norm(flat_ref)))
+            parity["ok"] = bool(parity["ok"] and parity["vs_unquantized_rel_l2"] < 0.03
+                                and parity["vs_unquantized_cosine"] > 0.995)
         sample_flop = 4 * h * d * rows.size * n
         cpu_baseline = {"value": sample_flop / cpu_s / 1e12, "unit": "TFLOPS", "cores": args.cpu_workers,
                         "kind": "port",
@@ -879,7 +908,8 @@ def paged_main(args) -> int:
         log(f"paged parity: {parity}")
     steps = args.steps
     result = {
-        "metric": "effective TFLOPS, paged 158K-tok BF16 MHA, 256-token pages from an aligned page store",
+        "metric": "effective TFLOPS, paged 158K-tok BF16 MHA, 256-token pages from an aligned page store"
+                  + (", INT8 K/V pages" if storage == "int8" else ""),
         "value": round(tflops, 2),
         "unit": "TFLOPS",
         "n_gpus": 1,
@@ -893,8 +923,9 @@ def paged_main(args) -> int:
         "data": "synthetic: Q/K/V ~ N(0,1) bf16 seeded per 4,096-token chunk, 1% of key rows x8",
         "config": {
             "workload": f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}, {PAGED_PAGE_TOKENS}-token "
-                        f"pages in an aligned on-disk store (direct_io={direct_io}), 16 GiB DRAM page cache, "
-                        "I/O queue depth 4, 2 GiB HBM workspace, output kept in HBM",
+                        f"{storage.upper()} K/V pages in an aligned on-disk store (direct_io={direct_io}), "
+                        "16 GiB DRAM page cache, I/O queue depth 4, 2 GiB HBM workspace, output kept in HBM",
+            "kv_storage_dtype": storage,
             "q_chunk_tokens": stats.q_chunk_tokens,
             "kv_chunk_tokens": stats.kv_chunk_tokens,
             "direct_io": direct_io,
