@@ -168,9 +168,17 @@ struct Geometry {
   static constexpr int I8_DMA_PER_WAVE = (I8_DMAS + WAVES - 1) / WAVES;
   static constexpr int I8_GRANULES = TILE_KEYS * I8_GR;               // per tensor per tile
   static constexpr int I8_PER_THREAD = (I8_GRANULES + THREADS - 1) / THREADS;
-  // Granule swizzle: rows r..r+7 (r % 8 == 0) get 8 distinct XOR masks and
-  // rows r..r+3 (r % 4 == 0) masks that differ in bits 1-2.
-  __device__ static inline int swz(int row) { return (((row & 3) << 1) | ((row >> 2) & 1)) & (G - 1); }
+  // Granule swizzle for gfx950's 64-bank LDS.  A ds_read_b128 phase is 16
+  // lanes (16 consecutive rows, one logical granule) and a ds_read_b64_tr_b16
+  // phase 32 lanes (4 consecutive rows, a 64-byte block of 4 granules).
+  // Head dim 128 (16 granules per 256-byte row): the mask is a bijection over
+  // 16 consecutive rows (the 16 b128 lanes hit 16 distinct granules) and rows
+  // r..r+3 (r % 4 == 0) differ in bits 2-3 (their 64-byte blocks land in
+  // distinct banks).  Narrower rows: 8 distinct masks over 8 rows.
+  __device__ static inline int swz(int row) {
+    if constexpr (G == 16) return ((row & 3) << 2) | ((row >> 2) & 3);
+    return (((row & 3) << 1) | ((row >> 2) & 1)) & (G - 1);
+  }
   __device__ static inline int offset(int row, int granule) {
     return row * ROW_BYTES + ((granule ^ swz(row)) << 4);
   }
