@@ -1,8 +1,8 @@
 """CPU oracle of the streamed exact-attention path.  TEST INFRASTRUCTURE ONLY.
 
-This module is the checker for the GPU path: only ``tests/``,
-``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
-use it, and never as the thing that is measured or shipped.  The product
+This module is the reference the GPU path is checked against: only
+``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may use it, and never as the thing that is measured or shipped.  The product
 package (``stream-attn_amd/seqattn``) never imports it.
 
 Every function is a numpy restatement of the reference algorithm; each cites
