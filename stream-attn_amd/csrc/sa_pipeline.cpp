@@ -23,6 +23,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <functional>
 #include <string>
 #include <vector>
 
@@ -77,6 +78,10 @@ struct sa_pipeline {
   hipEvent_t q_ready = nullptr, q_free = nullptr;
   hipEvent_t kv_ready[3] = {}, kv_free[3] = {};
   hipEvent_t out_ready[2] = {}, out_free[2] = {};
+  // sa_pipeline_run with one output slot: the Q block buffer and the output
+  // slot take turns as a pass's Q block and output (ready: Q copied in;
+  // done: output finalized; free: output copied out).
+  hipEvent_t alt_ready[2] = {}, alt_done[2] = {}, alt_free[2] = {};
   bool q_pending = false;
   bool kv_pending[3] = {false, false, false};
   bool out_pending[2] = {false, false};
@@ -113,6 +118,9 @@ void release(sa_pipeline* p) {
   for (int i = 0; i < 2; ++i) {
     if (p->out_ready[i]) hipEventDestroy(p->out_ready[i]);
     if (p->out_free[i]) hipEventDestroy(p->out_free[i]);
+    if (p->alt_ready[i]) hipEventDestroy(p->alt_ready[i]);
+    if (p->alt_done[i]) hipEventDestroy(p->alt_done[i]);
+    if (p->alt_free[i]) hipEventDestroy(p->alt_free[i]);
   }
   for (hipEvent_t e : p->t_start) hipEventDestroy(e);
   for (hipEvent_t e : p->t_stop) hipEventDestroy(e);
@@ -207,11 +215,14 @@ struct KVSource {
 // cleared by the first launch.  Keys at or beyond `visible_end` are masked for
 // every query of the block under the bottom-right causal rule; their chunks
 // change nothing and are neither copied nor launched, except that a chunk
-// always runs while the state is uninitialized.
+// always runs while the state is uninitialized.  `after_copy`, if given, is
+// called with the chunk's ordinal once its H2D copies are enqueued, so the
+// caller can slot other H2D work between chunks.
 int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, const KVSource& src,
                    int32_t kv_tokens, int32_t kv_local_offset, bool* initialize,
                    int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
-                   int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
+                   int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
+                   const std::function<int32_t(int32_t)>* after_copy = nullptr) {
   if (kv_tokens < 0 || kv_local_offset < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad K/V span kv_tokens=%d kv_local_offset=%d q_tokens=%d", kv_tokens,
                   kv_local_offset, q_tokens);
@@ -242,6 +253,10 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
                                    bytes, hipMemcpyHostToDevice, p->h2d));
       SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
       add_stats(st, 2 * bytes, 0, 0, 1, 0);
+      if (after_copy) {
+        const int32_t hrc = (*after_copy)(start / p->kv_chunk);
+        if (hrc != 0) return hrc;
+      }
       SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
       rc = launch_timed(p, q, sq_t, sq_h, p->k_slots[slot], kt, p->head_dim, p->v_slots[slot], kt,
                         p->head_dim, q_tokens, n, q_local_offset, (int32_t)position, causal_shift,
@@ -365,20 +380,22 @@ int32_t init_state(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, in
 
 int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_t k_length,
                   int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
-                  int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
+                  int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
+                  const void* q_block = nullptr,
+                  const std::function<int32_t(int32_t)>* after_copy = nullptr) {
   if (k_length < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad stream_kv sizes k_length=%d q_tokens=%d", k_length, q_tokens);
     return SA_ERR_INVALID_ARGUMENT;
   }
+  const void* q = q_block ? q_block : p->q_buffer;
   const int64_t qt = (int64_t)p->q_heads * p->head_dim;
   KVSource src{static_cast<const char*>(k_host), static_cast<const char*>(v_host), false, 0, 0, 0, 0};
   bool initialize = true;
-  int32_t rc = apply_span(p, p->q_buffer, qt, p->head_dim, src, k_length, 0, &initialize,
-                          q_tokens, q_local_offset, causal_shift, scale, causal, compute, st);
+  int32_t rc = apply_span(p, q, qt, p->head_dim, src, k_length, 0, &initialize, q_tokens, q_local_offset,
+                          causal_shift, scale, causal, compute, st, after_copy);
   if (rc != 0) return rc;
   if (initialize)
-    return init_state(p, p->q_buffer, qt, p->head_dim, q_tokens, q_local_offset, causal_shift,
-                      scale, compute);
+    return init_state(p, q, qt, p->head_dim, q_tokens, q_local_offset, causal_shift, scale, compute);
   return 0;
 }
 
@@ -420,6 +437,82 @@ int32_t d2h(sa_pipeline* p, void* dst, const void* src, int64_t bytes, int32_t s
     p->q_pending = true;
   }
   add_stats(st, 0, bytes, 0, 0, 0);
+  return 0;
+}
+
+// One Q block of sa_pipeline_run: rows [qt, qt + n) of the packed Q, with
+// its segment's K/V rows [k_start, k_start + k_len).
+struct Pass {
+  int64_t qt, k_start;
+  int32_t n, k_len, q_local, causal_shift;
+};
+
+// sa_pipeline_run with one output slot.  The plan's two block-sized buffers
+// (the Q block and the output slot) take turns: pass i reads its Q block from
+// buffer i % 2, is finalized into that same buffer (its Q rows are no longer
+// read by then) and copied out from it.  The next pass's Q block is copied
+// into the other buffer during pass i, in four pieces placed between K/V
+// chunk copies from the second chunk on, so each piece fits in the slack of
+// the K/V ring.  A pass therefore starts as soon as the previous one is
+// finalized: its Q block and first K/V chunks are already in HBM.  Memory and
+// decomposition are the plan's; only the order of the copies changes.
+int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const char* vh, char* oh,
+                        float* lse, int64_t lse_sh, const std::vector<Pass>& passes, double scale,
+                        int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
+  constexpr int kPieces = 4;
+  void* buf[2] = {p->q_buffer, p->out_slots[0]};
+  bool pending[2] = {false, false};  // a copy-out from the buffer was enqueued
+  // Work another entry point left on these buffers completes first.
+  if (p->q_pending) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->q_free, 0));
+  if (p->out_pending[0]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->out_free[0], 0));
+  auto copy_piece = [&](size_t i, int j) -> int32_t {
+    const Pass& ps = passes[i];
+    const int b = (int)(i & 1);
+    if (j == 0 && pending[b]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->alt_free[b], 0));
+    const int64_t r0 = (int64_t)ps.n * j / kPieces, r1 = (int64_t)ps.n * (j + 1) / kPieces;
+    const int64_t bytes = (r1 - r0) * p->q_row_bytes;
+    if (bytes > 0)
+      SA_HIP_RETURN(hipMemcpyAsync(static_cast<char*>(buf[b]) + r0 * p->q_row_bytes,
+                                   qh + (ps.qt + r0) * p->q_row_bytes, bytes, hipMemcpyHostToDevice, p->h2d));
+    const bool last = j == kPieces - 1;
+    add_stats(st, bytes, 0, last ? 1 : 0, 0, last ? ps.n : 0);
+    if (last) SA_HIP_RETURN(hipEventRecord(p->alt_ready[b], p->h2d));
+    return 0;
+  };
+  int32_t rc = 0;
+  if (!passes.empty()) {
+    for (int j = 0; j < kPieces && rc == 0; ++j) rc = copy_piece(0, j);
+    if (rc) return rc;
+  }
+  const int64_t q_stride = (int64_t)p->q_heads * p->head_dim;
+  for (size_t i = 0; i < passes.size(); ++i) {
+    const Pass& ps = passes[i];
+    const int b = (int)(i & 1);
+    const bool has_next = i + 1 < passes.size();
+    int next_piece = 0;
+    std::function<int32_t(int32_t)> between_chunks = [&](int32_t ordinal) -> int32_t {
+      if (!has_next || ordinal < 1 || next_piece >= kPieces) return 0;
+      return copy_piece(i + 1, next_piece++);
+    };
+    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->alt_ready[b], 0));
+    rc = stream_kv(p, kh + ps.k_start * p->kv_row_bytes, vh + ps.k_start * p->kv_row_bytes, ps.k_len, ps.n,
+                   ps.q_local, ps.causal_shift, scale, causal, compute, st, buf[b], &between_chunks);
+    if (rc) return rc;
+    while (has_next && next_piece < kPieces)
+      if ((rc = copy_piece(i + 1, next_piece++)) != 0) return rc;
+    rc = sa::launch_finalize(p->acc, p->m, p->l, buf[b], lse, q_stride, p->head_dim, p->q_heads, 1, q_stride,
+                             p->head_dim, lse_sh, ps.qt, ps.n, p->q_heads, p->head_dim, p->dtype, compute);
+    if (rc) return rc;
+    SA_HIP_RETURN(hipEventRecord(p->alt_done[b], compute));
+    SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->alt_done[b], 0));
+    const int64_t bytes = (int64_t)ps.n * p->q_row_bytes;
+    if (bytes > 0)
+      SA_HIP_RETURN(hipMemcpyAsync(oh + ps.qt * p->q_row_bytes, buf[b], bytes, hipMemcpyDeviceToHost, p->d2h));
+    SA_HIP_RETURN(hipEventRecord(p->alt_free[b], p->d2h));
+    pending[b] = true;
+    add_stats(st, 0, bytes, 0, 0, 0);
+  }
+  SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
   return 0;
 }
 
@@ -527,6 +620,11 @@ int32_t sa_pipeline_create(sa_pipeline** out_pipeline, int32_t device, void* q_b
   for (int i = 0; i < num_output_buffers && err == hipSuccess; ++i) {
     err = hipEventCreateWithFlags(&p->out_ready[i], flags);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&p->out_free[i], flags);
+  }
+  for (int i = 0; i < 2 && err == hipSuccess; ++i) {
+    err = hipEventCreateWithFlags(&p->alt_ready[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->alt_done[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->alt_free[i], flags);
   }
   if (err != hipSuccess) {
     int32_t rc = sa::hip_status(err, "sa_pipeline_create stream/event creation");
@@ -839,6 +937,22 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
   const char* kh = static_cast<const char*>(k_host);
   const char* vh = static_cast<const char*>(v_host);
   char* oh = static_cast<char*>(out_host);
+  if (p->has_out_slots && p->num_out == 1) {
+    std::vector<Pass> passes;
+    for (int32_t s = 0; s < num_segments; ++s) {
+      const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
+      const int64_t k_start = cu_seqlens_k[s], k_stop = cu_seqlens_k[s + 1];
+      const int64_t q_length = q_stop - q_start, k_length = k_stop - k_start;
+      if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0)) {
+        sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
+        return SA_ERR_INVALID_ARGUMENT;
+      }
+      for (int64_t qt = q_start; qt < q_stop; qt += p->q_chunk)
+        passes.push_back(Pass{qt, k_start, (int32_t)std::min<int64_t>(p->q_chunk, q_stop - qt), (int32_t)k_length,
+                              (int32_t)(qt - q_start), (int32_t)(k_length - q_length)});
+    }
+    return run_alternating(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
+  }
   int64_t chunk_index = 0;
   for (int32_t s = 0; s < num_segments; ++s) {
     const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
