@@ -191,6 +191,36 @@ def test_device_resident_inputs_are_bit_identical_to_streamed(causal):
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_one_and_two_output_slots_give_identical_results(causal):
+    """With one output slot the pipeline alternates the Q block buffer and the
+    slot between passes and copies the next Q block in pieces between K/V
+    chunks; with two slots it keeps the executor's order.  Many passes over
+    three segments (one empty) must agree bit for bit and match the oracle."""
+    announce(f"output slots 1 vs 2 causal={causal}")
+    gen = torch.Generator().manual_seed(61)
+    q = pinned_randn((701, 4, 128), torch.bfloat16, gen)
+    k = pinned_randn((650, 2, 128), torch.bfloat16, gen)
+    v = pinned_randn((650, 2, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 290, 290, 701], dtype=torch.int32)
+    cu_k = torch.tensor([0, 260, 260, 650], dtype=torch.int32)
+    results = []
+    for slots in (1, 2):
+        config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=64, kv_chunk_tokens=48,
+                                          num_output_buffers=slots)
+        out, lse, runner = run(q, k, v, cu_q, cu_k, config, causal=causal)
+        assert runner.plan.num_output_buffers == slots
+        # A second call on the same runner reuses the buffers in their new roles.
+        out2, lse2 = runner(q, k, v, cu_q, cu_k, causal=causal, return_lse=True)
+        torch.testing.assert_close(out2, out, atol=0, rtol=0)
+        torch.testing.assert_close(lse2, lse, atol=0, rtol=0)
+        results.append((out, lse))
+    torch.testing.assert_close(results[0][0], results[1][0], atol=0, rtol=0)
+    torch.testing.assert_close(results[0][1], results[1][1], atol=0, rtol=0)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=64, kv_chunk=48, causal=causal)
+    check(results[0][0], results[0][1], ref_o, ref_l)
+
+
 @pytest.mark.parametrize("scale", [-0.2, 0.0, 1e-3])
 def test_negative_zero_and_tiny_softmax_scales(scale):
     """The kernel folds a negative scale into the sign of Q and treats a zero
