@@ -32,6 +32,7 @@ Also reported, from the same run:
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import math
 import os
@@ -508,8 +509,14 @@ def sweep_main(args) -> int:
     cu = torch.tensor([0, n], dtype=torch.int32)
     rows = []
     published = {1: 206.3, 2: 217.4, 4: 218.5, 8: 218.2, 14: 218.9}  # README.md:61-68 (RTX 5090)
+    # One page-locked output for all budgets, and each budget's workspace
+    # returned to the device before the next is allocated, so every point
+    # starts from the same host and device memory state.
+    host_out = torch.empty((n, h, d), dtype=q.dtype, pin_memory=True)
     for gib in (1, 2, 4, 8, 14):
-        plan, out, stats, sec = run_pinned(q, k, v, cu, gib, None, args.steps, args.warmup)
+        gc.collect()
+        torch.cuda.empty_cache()
+        plan, out, stats, sec = run_pinned(q, k, v, cu, gib, None, args.steps, args.warmup, out=host_out)
         tflops = flop / sec / 1e12
         rows.append({"workspace_gib": gib, "q_chunk_tokens": plan.q_chunk_tokens,
                      "kv_chunk_tokens": plan.kv_chunk_tokens, "q_passes": plan.q_passes,

@@ -15,6 +15,7 @@ from __future__ import annotations
 import torch
 
 from ..config import ProjectionPipelineConfig
+from ..streaming.workspace import copy_streams
 
 
 class ProjectionWorkspace:
@@ -32,8 +33,9 @@ class ProjectionWorkspace:
             for _ in range(config.num_projection_buffers)
         ]
         self.compute_stream = torch.cuda.current_stream(device)
-        self.h2d_stream = torch.cuda.Stream(device=device)
-        self.d2h_stream = torch.cuda.Stream(device=device)
+        # The per-device copy stream pair shared with the attention pipeline
+        # (the projection copies and the attention copies do not overlap).
+        self.h2d_stream, self.d2h_stream = copy_streams(device)
         self.input_ready = [torch.cuda.Event() for _ in self.hidden]
         self.projected_ready = [torch.cuda.Event() for _ in self.hidden]
         self.copy_done = [torch.cuda.Event() for _ in self.hidden]

@@ -20,6 +20,28 @@ from .. import _native
 from ..planner import AttentionPlan
 
 
+_COPY_STREAMS: dict[int, tuple[torch.cuda.Stream, torch.cuda.Stream]] = {}
+
+
+def copy_streams(device: torch.device) -> tuple[torch.cuda.Stream, torch.cuda.Stream]:
+    """The (H2D, D2H) copy streams of ``device``, created once per process.
+
+    HIP maps streams onto a few hardware queues (GPU_MAX_HW_QUEUES, 4 by
+    default) in creation order. A fresh pair per workspace walks that
+    assignment, so after a few runners a copy stream can land on the compute
+    stream's queue; its copies then wait behind kernels instead of
+    overlapping them. Every workspace on a device shares this pair instead.
+    Copies of different pipelines on the pair run in FIFO order; each
+    pipeline's own events still order its copies against its kernels.
+    """
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    pair = _COPY_STREAMS.get(index)
+    if pair is None:
+        pair = (torch.cuda.Stream(device=index), torch.cuda.Stream(device=index))
+        _COPY_STREAMS[index] = pair
+    return pair
+
+
 class CudaWorkspace:
     def __init__(self, plan: AttentionPlan) -> None:
         device = plan.device
@@ -44,8 +66,7 @@ class CudaWorkspace:
         # Copy streams are torch streams (default priority) so torch's caching
         # allocator can track their uses of workspace and consumer buffers
         # (record_stream) for as long as those buffers live.
-        self.h2d_stream = torch.cuda.Stream(device=device)
-        self.d2h_stream = torch.cuda.Stream(device=device)
+        self.h2d_stream, self.d2h_stream = copy_streams(device)
 
         lib = _native.lib()
         k_ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in self.k])
@@ -79,4 +100,4 @@ class CudaWorkspace:
             pass
 
 
-__all__ = ["CudaWorkspace"]
+__all__ = ["CudaWorkspace", "copy_streams"]
