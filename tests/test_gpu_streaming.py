@@ -191,6 +191,39 @@ def test_device_resident_inputs_are_bit_identical_to_streamed(causal):
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
 
+def test_runners_share_one_copy_stream_pair_and_still_agree():
+    """Every workspace on a device uses the same H2D / D2H streams (fresh
+    streams per runner can land on the compute stream's hardware queue).
+    Runners interleaved on the shared pair give the results of a lone one."""
+    announce("shared copy streams")
+    gen = torch.Generator().manual_seed(67)
+    q = pinned_randn((400, 4, 128), torch.bfloat16, gen)
+    k = pinned_randn((380, 4, 128), torch.bfloat16, gen)
+    v = pinned_randn((380, 4, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 400], dtype=torch.int32)
+    cu_k = torch.tensor([0, 380], dtype=torch.int32)
+    configs = [StreamingAttentionConfig(backend="hip", q_chunk_tokens=qc, kv_chunk_tokens=kc)
+               for qc, kc in ((64, 48), (128, 96), (96, 64))]
+    runners, outs = [], []
+    for config in configs:
+        out, lse, runner = run(q, k, v, cu_q, cu_k, config)
+        runners.append(runner)
+        outs.append((out, lse))
+    streams = {(r._workspace.h2d_stream.cuda_stream, r._workspace.d2h_stream.cuda_stream) for r in runners}
+    assert len(streams) == 1, streams
+    h2d, d2h = next(iter(streams))
+    assert h2d != d2h
+    # Second round, runners alternating on the shared pair.
+    for runner, (out, lse) in zip(runners, outs):
+        out2, lse2 = runner(q, k, v, cu_q, cu_k, return_lse=True)
+        torch.testing.assert_close(out2, out, atol=0, rtol=0)
+        torch.testing.assert_close(lse2, lse, atol=0, rtol=0)
+    for (out, lse), config in zip(outs, configs):
+        ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=config.q_chunk_tokens,
+                              kv_chunk=config.kv_chunk_tokens, causal=False)
+        check(out, lse, ref_o, ref_l)
+
+
 @pytest.mark.parametrize("causal", [False, True])
 def test_one_and_two_output_slots_give_identical_results(causal):
     """With one output slot the pipeline alternates the Q block buffer and the
