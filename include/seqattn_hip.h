@@ -306,8 +306,11 @@ int32_t sa_pipeline_stream_kv_gather_int8(sa_pipeline* pipeline, const void* con
  * super-block / K/V chunk decomposition as sa_pipeline_run, using the
  * pipeline's state buffers; K/V chunks and Q blocks are read in place and
  * each block is finalized straight into out (and lse when non-NULL, layout
- * [q_heads, total_q] with row stride lse_stride_h).  Enqueued on
- * compute_stream; returns without waiting.  The reference accepts host
+ * [q_heads, total_q] with row stride lse_stride_h).  When kv_chunk_tokens is
+ * a multiple of 64, each Q block is one update launch over all keys of its
+ * segment that merges the row sums at every chunk boundary, so the result
+ * equals sa_pipeline_run's bit for bit.  Enqueued on compute_stream; returns
+ * without waiting.  The reference accepts host
  * tensors only (validation.py:13-14); this is the device-input extension.
  */
 int32_t sa_pipeline_run_resident(sa_pipeline* pipeline, const void* q, const void* k,

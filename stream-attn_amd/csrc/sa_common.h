@@ -58,7 +58,7 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
-                      hipStream_t stream);
+                      hipStream_t stream, int32_t merge_keys = 0);
 int32_t launch_update_int8(const void* q, const void* k, const void* v, const void* k_scales,
                            const void* v_scales, float* m, float* l, float* acc, int64_t sq_t,
                            int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t, int64_t sv_h,

@@ -123,6 +123,12 @@ struct UpdateParams {
   const uint16_t* vs;
   int64_t sks_g, sks_h, svs_g, svs_h;
   int32_t scale_offset, scale_shift;
+  // 16-bit launches spanning several K/V chunks of the streamed schedule:
+  // the tile count of one chunk (0: one chunk).  At each chunk boundary the
+  // two lane halves' partial row sums are merged exactly as a chunk launch
+  // stores l and the next one reloads it, so the result equals the chunked
+  // schedule's bit for bit.
+  int32_t merge_tiles = 0;
 };
 
 // Row r (0..15) of a 32x32 C tile held in register i of a lane in half h.
@@ -472,6 +478,7 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
 
   if constexpr (!QUANT) {
     // Tile t is computed from `cur` while tile t+1 streams into `next`.
+    int until_merge = p.merge_tiles;  // tiles left in the current K/V chunk
     auto tile = [&](int t, const uint8_t* cur, uint8_t* next) {
       // Every wave waits for its own DMA of tile t before the barrier, so
       // after it all 64 rows of `cur` are in LDS.  LDS DMA is counted by
@@ -483,6 +490,14 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
       __syncthreads();
       if (t + 1 < ntiles) issue_tile((t + 1) * Geo::TILE_KEYS, next);
       compute(t, cur);
+      if (p.merge_tiles > 0 && --until_merge == 0) {
+        until_merge = p.merge_tiles;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float full = l_part[qb] + __shfl_xor(l_part[qb], 32);
+          l_part[qb] = hf == 0 ? full : 0.f;
+        }
+      }
     };
     if (ntiles > 0) issue_tile(0, lds_a);
     for (int t = 0; t < ntiles; t += 2) {
@@ -724,7 +739,7 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
-                      hipStream_t stream) {
+                      hipStream_t stream, int32_t merge_keys) {
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
     set_error("sa_update_attention_state: unsupported dtype code %d", dtype);
     return SA_ERR_UNSUPPORTED_DTYPE;
@@ -779,6 +794,11 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
   p.kv_local_offset = kv_local_offset;
   p.causal_shift = causal_shift;
   p.scale_log2 = (float)(softmax_scale * 1.4426950408889634);
+  if (merge_keys < 0 || merge_keys % 64 != 0) {
+    set_error("merge_keys %d is not a multiple of the 64-key tile", merge_keys);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  p.merge_tiles = merge_keys / 64;
   const int dp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
   p.q_heads = q_heads;
   const bool causal = (flags & SA_FLAG_CAUSAL) != 0;

@@ -168,18 +168,21 @@ def test_host_aliased_and_device_resident_outputs_are_bit_identical_to_host_mode
     check(results[0][0], results[0][1], ref_o, ref_l)
 
 
+@pytest.mark.parametrize("kv_chunk", [96, 128])
 @pytest.mark.parametrize("causal", [False, True])
-def test_device_resident_inputs_are_bit_identical_to_streamed(causal):
-    """HBM-resident Q/K/V run the same Q-block / K/V-chunk schedule in place:
-    output and LSE equal the pinned-host streamed run bit for bit."""
-    announce(f"device-resident inputs causal={causal}")
+def test_device_resident_inputs_are_bit_identical_to_streamed(causal, kv_chunk):
+    """HBM-resident Q/K/V give the pinned-host streamed run's output and LSE
+    bit for bit.  With a 128-key chunk (a multiple of the 64-key tile) each Q
+    block is one launch over all keys that merges the row sums at every chunk
+    boundary; with 96 it is one launch per chunk, as in the streamed run."""
+    announce(f"device-resident inputs causal={causal} kv_chunk={kv_chunk}")
     gen = torch.Generator().manual_seed(37)
     q = pinned_randn((611, 8, 128), torch.bfloat16, gen)
     k = pinned_randn((540, 2, 128), torch.bfloat16, gen)
     v = pinned_randn((540, 2, 128), torch.bfloat16, gen)
     cu_q = torch.tensor([0, 200, 200, 611], dtype=torch.int32)
     cu_k = torch.tensor([0, 150, 150, 540], dtype=torch.int32)
-    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=160, kv_chunk_tokens=96)
+    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=160, kv_chunk_tokens=kv_chunk)
     out, lse, runner = run(q, k, v, cu_q, cu_k, config, causal=causal)
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     out_d, lse_d = runner(qd, kd, vd, cu_q, cu_k, causal=causal, return_lse=True)
@@ -187,7 +190,7 @@ def test_device_resident_inputs_are_bit_identical_to_streamed(causal):
     assert out_d.device.type == "cuda"
     torch.testing.assert_close(out_d.cpu(), out, atol=0, rtol=0)
     torch.testing.assert_close(lse_d.cpu(), lse, atol=0, rtol=0)
-    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=160, kv_chunk=96, causal=causal)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=160, kv_chunk=kv_chunk, causal=causal)
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
 
