@@ -307,10 +307,12 @@ int32_t sa_pipeline_stream_kv_gather_int8(sa_pipeline* pipeline, const void* con
  * pipeline's state buffers; K/V chunks and Q blocks are read in place and
  * each block is finalized straight into out (and lse when non-NULL, layout
  * [q_heads, total_q] with row stride lse_stride_h).  When kv_chunk_tokens is
- * a multiple of 64, each Q block is one update launch over all keys of its
- * segment that merges the row sums at every chunk boundary, so the result
- * equals sa_pipeline_run's bit for bit.  Enqueued on compute_stream; returns
- * without waiting.  The reference accepts host
+ * a multiple of 64 and out is 16-byte aligned with strides that are multiples
+ * of 8, each segment is one update launch over all of its queries and keys
+ * that finalizes in its epilogue and merges the row sums at every chunk
+ * boundary, so the result equals sa_pipeline_run's bit for bit; the state
+ * buffers are then untouched.  Enqueued on compute_stream; returns without
+ * waiting.  The reference accepts host
  * tensors only (validation.py:13-14); this is the device-input extension.
  */
 int32_t sa_pipeline_run_resident(sa_pipeline* pipeline, const void* q, const void* k,

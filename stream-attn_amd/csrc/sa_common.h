@@ -52,13 +52,24 @@ class DeviceGuard {
 
 // Kernel entry points shared between the kernel and pipeline translation units.
 namespace sa {
+// Output of an update launch that also finalizes its rows (launch_update with
+// SA_FLAG_INITIALIZE over all keys): out [q_tokens, q_heads, head_dim] with
+// strides (so_t, so_h, 1); lse element (h, t) at lse[h * lse_sh + lse_off + t]
+// when lse is non-null.
+struct FusedOutput {
+  void* out;
+  int64_t so_t, so_h;
+  float* lse;
+  int64_t lse_sh, lse_off;
+};
 int32_t launch_update(const void* q, const void* k, const void* v, float* m, float* l, float* acc,
                       int64_t sq_t, int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t,
                       int64_t sv_h, int64_t ss_t, int64_t ss_h, int64_t sa_t, int64_t sa_h,
                       int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
-                      hipStream_t stream, int32_t merge_keys = 0);
+                      hipStream_t stream, int32_t merge_keys = 0,
+                      const FusedOutput* fused = nullptr);
 int32_t launch_update_int8(const void* q, const void* k, const void* v, const void* k_scales,
                            const void* v_scales, float* m, float* l, float* acc, int64_t sq_t,
                            int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t, int64_t sv_h,

@@ -129,6 +129,15 @@ struct UpdateParams {
   // stores l and the next one reloads it, so the result equals the chunked
   // schedule's bit for bit.
   int32_t merge_tiles = 0;
+  // Fused finalize, for launches that start the state and cover every key of
+  // their rows: when out is non-null the epilogue writes acc / l (0 where
+  // l == 0) to out and, when lse is non-null, (m + log2 l) ln 2 (-inf where
+  // l == 0) to lse[head * lse_sh + lse_off + query], with the expressions of
+  // finalize_kernel, and stores no state.
+  uint16_t* out = nullptr;
+  int64_t so_t = 0, so_h = 0;
+  float* lse = nullptr;
+  int64_t lse_sh = 0, lse_off = 0;
 };
 
 // Row r (0..15) of a 32x32 C tile held in register i of a lane in half h.
@@ -215,7 +224,10 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
   const int logical = (b & 7) * p.xcd_run + (b >> 3);
   if (logical >= p.q_blocks * p.q_heads) return;
   const int head = logical / p.q_blocks;
-  const int q_block = (logical - head * p.q_blocks) * Geo::BLOCK_M;
+  // Under a causal mask later query blocks see more keys: they are dealt
+  // first so that the short blocks fill the end of the launch.
+  const int qb_index = CAUSAL ? p.q_blocks - 1 - (logical - head * p.q_blocks) : logical - head * p.q_blocks;
+  const int q_block = qb_index * Geo::BLOCK_M;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -624,6 +636,29 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
   for (int qb = 0; qb < QB; ++qb) {
     const float l_full = l_part[qb] + __shfl_xor(l_part[qb], 32);
     if (qi[qb] >= p.q_tokens) continue;
+    if (p.out != nullptr) {
+      uint16_t* orow = p.out + (int64_t)qi[qb] * p.so_t + (int64_t)head * p.so_h;
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int col = 32 * d + 8 * g + 4 * hf;
+          if (col < p.head_dim) {
+            const f32x16& a = acc[qb][d];
+            u32x2 o = {0, 0};
+            if (l_full > 0.f) {
+              o[0] = Op::pack2(a[4 * g + 0] / l_full, a[4 * g + 1] / l_full);
+              o[1] = Op::pack2(a[4 * g + 2] / l_full, a[4 * g + 3] / l_full);
+            }
+            *reinterpret_cast<u32x2*>(orow + col) = o;
+          }
+        }
+      }
+      if (p.lse != nullptr && hf == 0)
+        p.lse[(int64_t)head * p.lse_sh + p.lse_off + qi[qb]] =
+            l_full > 0.f ? (m_run[qb] + log2f(l_full)) * 0.69314718055994530942f : -INFINITY;
+      continue;
+    }
     const int64_t srow = (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
     if (hf == 0) {
       p.m[srow] = m_run[qb];
@@ -739,7 +774,7 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
-                      hipStream_t stream, int32_t merge_keys) {
+                      hipStream_t stream, int32_t merge_keys, const FusedOutput* fused) {
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
     set_error("sa_update_attention_state: unsupported dtype code %d", dtype);
     return SA_ERR_UNSUPPORTED_DTYPE;
@@ -799,6 +834,26 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
     return SA_ERR_INVALID_ARGUMENT;
   }
   p.merge_tiles = merge_keys / 64;
+  if (fused != nullptr) {
+    // Same output layout rules as the finalize kernel.
+    if (!(flags & SA_FLAG_INITIALIZE) || !fused->out || fused->so_t % 8 != 0 || fused->so_h % 8 != 0 ||
+        !aligned(fused->out, 16)) {
+      set_error("fused finalize needs an initializing launch and a 16-byte aligned output with "
+                "vector-aligned strides");
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    p.out = static_cast<uint16_t*>(fused->out);
+    p.so_t = fused->so_t;
+    p.so_h = fused->so_h;
+    p.lse = fused->lse;
+    p.lse_sh = fused->lse_sh;
+    p.lse_off = fused->lse_off;
+  }
+  // Workgroup numbering is 32-bit: at least 128 queries per workgroup.
+  if (((int64_t)q_tokens + 127) / 128 * q_heads > (int64_t)INT32_MAX / 8) {
+    set_error("sa_update_attention_state: q_tokens * q_heads too large for one launch");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
   const int dp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : head_dim <= 128 ? 128 : 256;
   p.q_heads = q_heads;
   const bool causal = (flags & SA_FLAG_CAUSAL) != 0;

@@ -152,7 +152,8 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
                      int64_t sk_t, int64_t sk_h, const void* v, int64_t sv_t, int64_t sv_h,
                      int32_t q_tokens, int32_t kv_tokens, int32_t q_local_offset,
                      int32_t kv_local_offset, int32_t causal_shift, double scale, int32_t flags,
-                     hipStream_t compute, int32_t merge_keys = 0) {
+                     hipStream_t compute, int32_t merge_keys = 0,
+                     const sa::FusedOutput* fused = nullptr) {
   if (p->timing) {
     if (p->t_used == p->t_start.size()) {
       hipEvent_t a = nullptr, b = nullptr;
@@ -167,7 +168,7 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
   int32_t rc = sa::launch_update(q, k, v, p->m, p->l, p->acc, sq_t, sq_h, sk_t, sk_h, sv_t, sv_h,
                                  p->q_heads, 1, qt, p->head_dim, q_tokens, kv_tokens, p->q_heads,
                                  p->kv_heads, p->head_dim, q_local_offset, kv_local_offset,
-                                 causal_shift, scale, flags, p->dtype, compute, merge_keys);
+                                 causal_shift, scale, flags, p->dtype, compute, merge_keys, fused);
   if (rc != 0) return rc;
   if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
   return 0;
@@ -804,34 +805,42 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
     const int32_t causal_shift = (int32_t)(k_length - q_length);
     KVSource src{kd + k_start * stride_kt * 2, vd + k_start * stride_vt * 2, true,
                  stride_kt, stride_kh, stride_vt, stride_vh};
-    for (int64_t qs = q_start; qs < q_stop; qs += p->q_chunk) {
-      const int32_t n = (int32_t)std::min<int64_t>(p->q_chunk, q_stop - qs);
-      const char* qblock = qd + qs * stride_qt * 2;
-      bool initialize = true;
-      int32_t rc = 0;
-      if (p->kv_chunk % 64 == 0) {
-        // K/V already in HBM: one launch over the whole segment, merging the
-        // row sums at every kv_chunk boundary, gives the chunked schedule's
-        // result bit for bit without its per-chunk state round trips and
-        // per-launch tails.  Stats count the chunks the schedule covers.
-        const int64_t visible_end =
-            causal ? std::max<int64_t>(0, (int64_t)(qs - q_start) + n + causal_shift) : INT64_MAX;
+    char* seg_out = od + q_start * stride_ot * 2;
+    if (q_length > 0 && p->kv_chunk % 64 == 0 && q_length <= INT32_MAX && k_length <= INT32_MAX &&
+        stride_ot % 8 == 0 && stride_oh % 8 == 0 && reinterpret_cast<uintptr_t>(seg_out) % 16 == 0) {
+      // K/V already in HBM: one launch covers every query and key of the
+      // segment and finalizes its rows in the epilogue.  The row sums are
+      // merged at every kv_chunk boundary exactly as the chunked schedule
+      // stores and reloads them, so the output and LSE equal
+      // sa_pipeline_run's bit for bit, with no state round trips, no
+      // per-launch tails and no finalize launches.  Stats count the Q blocks
+      // and chunks of the chunked schedule.
+      const sa::FusedOutput fused{seg_out, stride_ot, stride_oh, lse, lse_stride_h, q_start};
+      int32_t rc = launch_timed(p, qd + q_start * stride_qt * 2, stride_qt, stride_qh, src.k, src.sk_t,
+                                src.sk_h, src.v, src.sv_t, src.sv_h, (int32_t)q_length, (int32_t)k_length, 0,
+                                0, causal_shift, softmax_scale,
+                                (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, p->kv_chunk,
+                                &fused);
+      if (rc != 0) return rc;
+      for (int64_t qs = q_start; qs < q_stop; qs += p->q_chunk) {
+        const int64_t n = std::min<int64_t>(p->q_chunk, q_stop - qs);
+        const int64_t visible_end = causal ? std::max<int64_t>(0, qs - q_start + n + causal_shift) : INT64_MAX;
         int64_t chunks = 0;
         for (int64_t start = 0; start < k_length; start += p->kv_chunk) {
           if (chunks > 0 && start >= visible_end) break;
           ++chunks;
         }
-        rc = launch_timed(p, qblock, stride_qt, stride_qh, src.k, src.sk_t, src.sk_h, src.v, src.sv_t, src.sv_h, n,
-                          (int32_t)k_length, (int32_t)(qs - q_start), 0, causal_shift, softmax_scale,
-                          (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, p->kv_chunk);
-        if (rc != 0) return rc;
-        add_stats(stats, 0, 0, 0, chunks, 0);
-        initialize = false;
-      } else {
-        rc = apply_span(p, qblock, stride_qt, stride_qh, src, (int32_t)k_length, 0, &initialize, n,
-                        (int32_t)(qs - q_start), causal_shift, softmax_scale, causal, compute, stats);
-        if (rc != 0) return rc;
+        add_stats(stats, 0, 0, 1, chunks, n);
       }
+      continue;
+    }
+    for (int64_t qs = q_start; qs < q_stop; qs += p->q_chunk) {
+      const int32_t n = (int32_t)std::min<int64_t>(p->q_chunk, q_stop - qs);
+      const char* qblock = qd + qs * stride_qt * 2;
+      bool initialize = true;
+      int32_t rc = apply_span(p, qblock, stride_qt, stride_qh, src, (int32_t)k_length, 0, &initialize, n,
+                              (int32_t)(qs - q_start), causal_shift, softmax_scale, causal, compute, stats);
+      if (rc != 0) return rc;
       if (initialize) {
         rc = init_state(p, qblock, stride_qt, stride_qh, n, (int32_t)(qs - q_start), causal_shift,
                         softmax_scale, compute);

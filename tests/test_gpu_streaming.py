@@ -194,6 +194,36 @@ def test_device_resident_inputs_are_bit_identical_to_streamed(causal, kv_chunk):
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
 
+@pytest.mark.parametrize("dtype,head_dim,q_heads,kv_heads", [
+    (torch.float16, 128, 4, 4),
+    (torch.bfloat16, 64, 6, 2),
+    (torch.bfloat16, 96, 4, 1),
+    (torch.bfloat16, 256, 2, 1),
+])
+def test_fused_resident_launch_matches_streamed_at_every_geometry(dtype, head_dim, q_heads, kv_heads):
+    """With device inputs and a K/V chunk that is a multiple of 64, each
+    segment is one launch that finalizes its rows in the epilogue.  At every
+    kernel geometry and both 16-bit dtypes it gives the pinned-host streamed
+    run's output and LSE bit for bit, causal, including the first segment's
+    200 queries that see no key (output 0, LSE -inf)."""
+    announce(f"fused resident launch {dtype} d={head_dim} heads={q_heads}/{kv_heads}")
+    gen = torch.Generator().manual_seed(41)
+    q = pinned_randn((700, q_heads, head_dim), dtype, gen)
+    k = pinned_randn((900, kv_heads, head_dim), dtype, gen)
+    v = pinned_randn((900, kv_heads, head_dim), dtype, gen)
+    cu_q = torch.tensor([0, 300, 700], dtype=torch.int32)
+    cu_k = torch.tensor([0, 100, 900], dtype=torch.int32)
+    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=192, kv_chunk_tokens=128)
+    out, lse, runner = run(q, k, v, cu_q, cu_k, config, causal=True)
+    out_d, lse_d = runner(q.cuda(), k.cuda(), v.cuda(), cu_q, cu_k, causal=True, return_lse=True)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(out_d.cpu(), out, atol=0, rtol=0)
+    torch.testing.assert_close(lse_d.cpu(), lse, atol=0, rtol=0)
+    assert torch.isneginf(lse_d[:, :200]).all() and (out_d[:200] == 0).all()
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=192, kv_chunk=128, causal=True)
+    check(out_d.cpu(), lse_d, ref_o, ref_l)
+
+
 def test_runners_share_one_copy_stream_pair_and_still_agree():
     """Every workspace on a device uses the same H2D / D2H streams (fresh
     streams per runner can land on the compute stream's hardware queue).
