@@ -14,8 +14,8 @@ Two legs run on the same inputs:
   schedule's bit for bit;
 * pinned (``pinned_dram_e2e``): the reference's own setting, caller-owned
   pinned DRAM to pinned DRAM through the 2 GiB workspace, K/V re-streamed over
-  PCIe for every pass, final D2H included; one update launch per (Q block,
-  K/V chunk).
+  PCIe for every pass, final D2H included; each K/V chunk is applied by two
+  concurrent launches, one per half of the Q block's rows, on two streams.
 
 Effective TFLOPS = 4 * heads * head_dim * tokens^2 / seconds per step (the
 reference's definition, benchmarking/streaming.py:206).  Prints ONE JSON line.
@@ -293,7 +293,11 @@ def main() -> int:
             "unit": "TFLOPS",
             "ms_per_step": round(sec * 1e3, 2),
             "vs_published_rtx5090": round(flop / sec / 1e12 / PUBLISHED_TFLOPS, 3),
+            # Two concurrent launches per K/V chunk (one per half of the Q
+            # block's rows); each duration includes the time the two share
+            # the GPU.
             "kernel_avg_launch_ms": round(kernel_ms / max(launches, 1), 4),
+            "update_launches_per_step": launches // max(steps, 1),
             "h2d_gb_per_step": round(h2d_per_step / 1e9, 2),
             "h2d_achieved_gbps": round(h2d_per_step / sec / 1e9, 2),
             "h2d_measured_gbps": round(h2d_peak, 2),

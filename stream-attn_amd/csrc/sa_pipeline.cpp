@@ -14,6 +14,15 @@
 //                (and q_free when the output lives in the Q buffer)
 // Copies are hipMemcpyAsync on two dedicated default-priority streams, so
 // PCIe traffic in both directions overlaps the kernels on the compute stream.
+//
+// Streamed chunks of a Q block of at least 512 rows are applied by two
+// launches, one per half of the block's rows: the first on the compute
+// stream, the second on the pipeline's own `side` stream (default priority).
+// A span forks `side` from the compute stream and joins it back, and a slot
+// is refilled only after both halves recorded their kv_free events.  The two
+// halves' launches run concurrently, so one launch's partial last round of
+// workgroups overlaps the other's work instead of leaving CUs idle.  Every
+// row's arithmetic is that of a single launch: results are bit-identical.
 
 #include <hip/hip_runtime.h>
 
@@ -77,6 +86,12 @@ struct sa_pipeline {
   bool owns_streams = false;
   hipEvent_t q_ready = nullptr, q_free = nullptr;
   hipEvent_t kv_ready[3] = {}, kv_free[3] = {};
+  // Second half of a split chunk update: its stream, the slot-free events it
+  // records, and the span's fork / join events.
+  hipStream_t side = nullptr;
+  hipEvent_t kv_free_side[3] = {};
+  hipEvent_t fork = nullptr, join = nullptr;
+  bool kv_side_pending[3] = {false, false, false};
   hipEvent_t out_ready[2] = {}, out_free[2] = {};
   // sa_pipeline_run with one output slot: the Q block buffer and the output
   // slot take turns as a pass's Q block and output (ready: Q copied in;
@@ -108,12 +123,14 @@ void add_stats(sa_pipeline_stats* st, int64_t h2d, int64_t d2h, int64_t qc, int6
 void release(sa_pipeline* p) {
   if (p->h2d) hipStreamSynchronize(p->h2d);
   if (p->d2h) hipStreamSynchronize(p->d2h);
-  hipEvent_t* evs[] = {&p->q_ready, &p->q_free};
+  if (p->side) hipStreamSynchronize(p->side);
+  hipEvent_t* evs[] = {&p->q_ready, &p->q_free, &p->fork, &p->join};
   for (hipEvent_t* e : evs)
     if (*e) hipEventDestroy(*e);
   for (int i = 0; i < 3; ++i) {
     if (p->kv_ready[i]) hipEventDestroy(p->kv_ready[i]);
     if (p->kv_free[i]) hipEventDestroy(p->kv_free[i]);
+    if (p->kv_free_side[i]) hipEventDestroy(p->kv_free_side[i]);
   }
   for (int i = 0; i < 2; ++i) {
     if (p->out_ready[i]) hipEventDestroy(p->out_ready[i]);
@@ -128,6 +145,15 @@ void release(sa_pipeline* p) {
     if (p->h2d) hipStreamDestroy(p->h2d);
     if (p->d2h) hipStreamDestroy(p->d2h);
   }
+  if (p->side) hipStreamDestroy(p->side);
+}
+
+// Make the H2D stream wait until ring slot `slot` is no longer read by any
+// launch (both halves of a split update).
+int32_t wait_slot_free(sa_pipeline* p, int slot) {
+  if (p->kv_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free[slot], 0));
+  if (p->kv_side_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free_side[slot], 0));
+  return 0;
 }
 
 int32_t load_q(sa_pipeline* p, const void* q_host, int32_t q_tokens, hipStream_t compute,
@@ -153,7 +179,7 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
                      int32_t q_tokens, int32_t kv_tokens, int32_t q_local_offset,
                      int32_t kv_local_offset, int32_t causal_shift, double scale, int32_t flags,
                      hipStream_t compute, int32_t merge_keys = 0,
-                     const sa::FusedOutput* fused = nullptr) {
+                     const sa::FusedOutput* fused = nullptr, int32_t state_row = 0) {
   if (p->timing) {
     if (p->t_used == p->t_start.size()) {
       hipEvent_t a = nullptr, b = nullptr;
@@ -165,7 +191,9 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
     SA_HIP_RETURN(hipEventRecord(p->t_start[p->t_used], compute));
   }
   const int64_t qt = (int64_t)p->q_heads * p->head_dim;
-  int32_t rc = sa::launch_update(q, k, v, p->m, p->l, p->acc, sq_t, sq_h, sk_t, sk_h, sv_t, sv_h,
+  const int64_t srow = (int64_t)state_row * p->q_heads;
+  int32_t rc = sa::launch_update(q, k, v, p->m + srow, p->l + srow, p->acc + srow * p->head_dim, sq_t,
+                                 sq_h, sk_t, sk_h, sv_t, sv_h,
                                  p->q_heads, 1, qt, p->head_dim, q_tokens, kv_tokens, p->q_heads,
                                  p->kv_heads, p->head_dim, q_local_offset, kv_local_offset,
                                  causal_shift, scale, flags, p->dtype, compute, merge_keys, fused);
@@ -232,6 +260,15 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
   int64_t visible_end = INT64_MAX;
   if (causal) visible_end = std::max<int64_t>(0, (int64_t)q_local_offset + q_tokens + causal_shift);
   const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+  // Rows [0, split) update on the compute stream, [split, q_tokens) on side;
+  // split is a multiple of 256 queries, the workgroup tile.
+  const int32_t split = (!src.on_device && q_tokens >= 512) ? (q_tokens / 2 + 255) / 256 * 256 : q_tokens;
+  const bool two = split < q_tokens && kv_tokens > 0;
+  const char* q_second = static_cast<const char*>(q) + (int64_t)split * sq_t * 2;
+  if (two) {
+    SA_HIP_RETURN(hipEventRecord(p->fork, compute));
+    SA_HIP_RETURN(hipStreamWaitEvent(p->side, p->fork, 0));
+  }
   for (int32_t start = 0; start < kv_tokens; start += p->kv_chunk) {
     const int64_t position = (int64_t)kv_local_offset + start;
     if (!*initialize && position >= visible_end) break;
@@ -247,7 +284,8 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
     } else {
       const int slot = (int)(p->ring_next++ % p->num_kv);
       const int64_t bytes = (int64_t)n * p->kv_row_bytes;
-      if (p->kv_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free[slot], 0));
+      int32_t wrc = wait_slot_free(p, slot);
+      if (wrc != 0) return wrc;
       SA_HIP_RETURN(hipMemcpyAsync(p->k_slots[slot], src.k + (int64_t)start * p->kv_row_bytes,
                                    bytes, hipMemcpyHostToDevice, p->h2d));
       SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], src.v + (int64_t)start * p->kv_row_bytes,
@@ -260,13 +298,26 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
       }
       SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
       rc = launch_timed(p, q, sq_t, sq_h, p->k_slots[slot], kt, p->head_dim, p->v_slots[slot], kt,
-                        p->head_dim, q_tokens, n, q_local_offset, (int32_t)position, causal_shift,
+                        p->head_dim, split, n, q_local_offset, (int32_t)position, causal_shift,
                         scale, flags, compute);
       if (rc != 0) return rc;
       SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
       p->kv_pending[slot] = true;
+      if (two) {
+        SA_HIP_RETURN(hipStreamWaitEvent(p->side, p->kv_ready[slot], 0));
+        rc = launch_timed(p, q_second, sq_t, sq_h, p->k_slots[slot], kt, p->head_dim, p->v_slots[slot], kt,
+                          p->head_dim, q_tokens - split, n, q_local_offset + split, (int32_t)position,
+                          causal_shift, scale, flags, p->side, 0, nullptr, split);
+        if (rc != 0) return rc;
+        SA_HIP_RETURN(hipEventRecord(p->kv_free_side[slot], p->side));
+        p->kv_side_pending[slot] = true;
+      }
     }
     *initialize = false;
+  }
+  if (two) {
+    SA_HIP_RETURN(hipEventRecord(p->join, p->side));
+    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->join, 0));
   }
   return 0;
 }
@@ -319,7 +370,8 @@ int32_t apply_gather(sa_pipeline* p, const void* const* k_frags, const void* con
     if (!*initialize && position >= visible_end) break;
     const int32_t n = (int32_t)std::min<int64_t>(p->kv_chunk, total - start);
     const int slot = (int)(p->ring_next++ % p->num_kv);
-    if (p->kv_pending[slot]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->kv_free[slot], 0));
+    int32_t wrc = wait_slot_free(p, slot);
+    if (wrc != 0) return wrc;
     char* kd = static_cast<char*>(p->k_slots[slot]);
     char* vd = static_cast<char*>(p->v_slots[slot]);
     int64_t filled = 0;
@@ -617,7 +669,11 @@ int32_t sa_pipeline_create(sa_pipeline** out_pipeline, int32_t device, void* q_b
   for (int i = 0; i < num_kv_buffers && err == hipSuccess; ++i) {
     err = hipEventCreateWithFlags(&p->kv_ready[i], flags);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&p->kv_free[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->kv_free_side[i], flags);
   }
+  if (err == hipSuccess) err = hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&p->fork, flags);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&p->join, flags);
   for (int i = 0; i < num_output_buffers && err == hipSuccess; ++i) {
     err = hipEventCreateWithFlags(&p->out_ready[i], flags);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&p->out_free[i], flags);

@@ -224,6 +224,45 @@ def test_fused_resident_launch_matches_streamed_at_every_geometry(dtype, head_di
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
 
+@pytest.mark.parametrize("num_kv", [1, 3])
+@pytest.mark.parametrize("causal", [False, True])
+def test_split_chunk_updates_on_two_streams_are_bit_identical(causal, num_kv):
+    """Streamed Q blocks of 512 rows or more apply each K/V chunk with two
+    launches, one per half of the rows, on two streams.  With a one-slot ring
+    the next copy must wait for both halves; with three slots the halves run
+    ahead of each other.  Host output, device-consumer output and the
+    HBM-resident single launch agree bit for bit."""
+    announce(f"split chunk updates causal={causal} num_kv={num_kv}")
+    gen = torch.Generator().manual_seed(43)
+    q = pinned_randn((1400, 4, 128), torch.bfloat16, gen)
+    k = pinned_randn((1300, 2, 128), torch.bfloat16, gen)
+    v = pinned_randn((1300, 2, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 1100, 1400], dtype=torch.int32)
+    cu_k = torch.tensor([0, 1000, 1300], dtype=torch.int32)
+    results, runners = [], []
+    for output_mode in ("host", "device_consumer"):
+        config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=1024, kv_chunk_tokens=256,
+                                          num_kv_buffers=num_kv, output_mode=output_mode)
+        plan = build_plan(q_heads=4, kv_heads=2, head_dim=128, dtype=q.dtype, device="cuda",
+                          max_q_tokens=q.shape[0], max_kv_tokens=k.shape[0], config=config)
+        runner = StreamingAttentionRunner(plan, config)
+        out = torch.empty_like(q).pin_memory()
+        if output_mode == "host":
+            runner(q, k, v, cu_q, cu_k, out=out, causal=causal)
+        else:
+            runner.run_with_device_output(q, k, v, cu_q, cu_k, output_transform=lambda a, s, e: a.reshape(-1, 4, 128),
+                                          out=out, causal=causal)
+        torch.cuda.synchronize()
+        results.append(out)
+        runners.append(runner)
+    out_d = runners[0](q.cuda(), k.cuda(), v.cuda(), cu_q, cu_k, causal=causal)
+    torch.cuda.synchronize()
+    torch.testing.assert_close(results[1], results[0], atol=0, rtol=0)
+    torch.testing.assert_close(out_d.cpu(), results[0], atol=0, rtol=0)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=1024, kv_chunk=256, causal=causal)
+    check(results[0], torch.from_numpy(ref_l), ref_o, ref_l)
+
+
 def test_runners_share_one_copy_stream_pair_and_still_agree():
     """Every workspace on a device uses the same H2D / D2H streams (fresh
     streams per runner can land on the compute stream's hardware queue).
