@@ -500,6 +500,20 @@ struct Pass {
   int32_t n, k_len, q_local, causal_shift;
 };
 
+// Rows per pass for a segment of q_length query rows: the pass count of
+// q_chunk-row blocks, with the rows spread evenly over the passes in
+// multiples of 256 queries (the update kernel's workgroup tile) instead of a
+// short last block.  A short pass applies every K/V chunk to few rows, so its
+// chunk copies outrun its kernels; even passes keep each chunk's copy hidden
+// behind its compute.  The pass count, and with it the H2D bytes, is that of
+// q_chunk-row blocks.
+int64_t pass_rows(int64_t q_length, int32_t q_chunk) {
+  if (q_length <= q_chunk) return q_chunk;
+  const int64_t passes = (q_length + q_chunk - 1) / q_chunk;
+  const int64_t even = (q_length + passes - 1) / passes;
+  return std::min<int64_t>(q_chunk, (even + 255) / 256 * 256);
+}
+
 // sa_pipeline_run with one output slot.  The plan's two block-sized buffers
 // (the Q block and the output slot) take turns: pass i reads its Q block from
 // buffer i % 2, is finalized into that same buffer (its Q rows are no longer
@@ -542,10 +556,29 @@ int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const ch
     const Pass& ps = passes[i];
     const int b = (int)(i & 1);
     const bool has_next = i + 1 < passes.size();
+    // The next pass's Q block goes into the buffer whose output the previous
+    // pass is still copying out, and the H2D stream runs in order, so piece 0
+    // waits for that copy and every K/V chunk copy after it waits too.  The
+    // pieces therefore follow chunks spread over the pass (after chunk
+    // (j + 1) * chunks / 5 for piece j), which leaves the output copy a fifth
+    // of the pass to finish before anything waits for it.
+    int64_t chunks = 0;
+    {
+      const int64_t visible_end =
+          causal ? std::max<int64_t>(0, (int64_t)ps.q_local + ps.n + ps.causal_shift) : INT64_MAX;
+      for (int64_t start = 0; start < ps.k_len; start += p->kv_chunk) {
+        if (chunks > 0 && start >= visible_end) break;
+        ++chunks;
+      }
+    }
     int next_piece = 0;
     std::function<int32_t(int32_t)> between_chunks = [&](int32_t ordinal) -> int32_t {
-      if (!has_next || ordinal < 1 || next_piece >= kPieces) return 0;
-      return copy_piece(i + 1, next_piece++);
+      while (has_next && next_piece < kPieces &&
+             ordinal >= std::max<int64_t>(1, (next_piece + 1) * chunks / (kPieces + 1))) {
+        const int32_t prc = copy_piece(i + 1, next_piece++);
+        if (prc != 0) return prc;
+      }
+      return 0;
     };
     SA_HIP_RETURN(hipStreamWaitEvent(compute, p->alt_ready[b], 0));
     rc = stream_kv(p, kh + ps.k_start * p->kv_row_bytes, vh + ps.k_start * p->kv_row_bytes, ps.k_len, ps.n,
@@ -878,8 +911,9 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
                                 (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, p->kv_chunk,
                                 &fused);
       if (rc != 0) return rc;
-      for (int64_t qs = q_start; qs < q_stop; qs += p->q_chunk) {
-        const int64_t n = std::min<int64_t>(p->q_chunk, q_stop - qs);
+      const int64_t block = pass_rows(q_length, p->q_chunk);
+      for (int64_t qs = q_start; qs < q_stop; qs += block) {
+        const int64_t n = std::min<int64_t>(block, q_stop - qs);
         const int64_t visible_end = causal ? std::max<int64_t>(0, qs - q_start + n + causal_shift) : INT64_MAX;
         int64_t chunks = 0;
         for (int64_t start = 0; start < k_length; start += p->kv_chunk) {
@@ -1032,8 +1066,9 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
         sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
         return SA_ERR_INVALID_ARGUMENT;
       }
-      for (int64_t qt = q_start; qt < q_stop; qt += p->q_chunk)
-        passes.push_back(Pass{qt, k_start, (int32_t)std::min<int64_t>(p->q_chunk, q_stop - qt), (int32_t)k_length,
+      const int64_t block = pass_rows(q_length, p->q_chunk);
+      for (int64_t qt = q_start; qt < q_stop; qt += block)
+        passes.push_back(Pass{qt, k_start, (int32_t)std::min<int64_t>(block, q_stop - qt), (int32_t)k_length,
                               (int32_t)(qt - q_start), (int32_t)(k_length - q_length)});
     }
     return run_alternating(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
@@ -1048,8 +1083,9 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
       return SA_ERR_INVALID_ARGUMENT;
     }
     const int32_t causal_shift = (int32_t)(k_length - q_length);
-    for (int64_t qt = q_start; qt < q_stop; qt += p->q_chunk) {
-      const int32_t n = (int32_t)std::min<int64_t>(p->q_chunk, q_stop - qt);
+    const int64_t block = pass_rows(q_length, p->q_chunk);
+    for (int64_t qt = q_start; qt < q_stop; qt += block) {
+      const int32_t n = (int32_t)std::min<int64_t>(block, q_stop - qt);
       int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
       if (rc) return rc;
       rc = stream_kv(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
