@@ -519,8 +519,8 @@ int64_t pass_rows(int64_t q_length, int32_t q_chunk) {
 // buffer i % 2, is finalized into that same buffer (its Q rows are no longer
 // read by then) and copied out from it.  The next pass's Q block is copied
 // into the other buffer during pass i, in four pieces placed between K/V
-// chunk copies from the second chunk on, so each piece fits in the slack of
-// the K/V ring.  A pass therefore starts as soon as the previous one is
+// chunk copies spread over the pass, so each piece fits in the slack of the
+// K/V ring.  A pass therefore starts as soon as the previous one is
 // finalized: its Q block and first K/V chunks are already in HBM.  Memory and
 // decomposition are the plan's; only the order of the copies changes.
 int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const char* vh, char* oh,
