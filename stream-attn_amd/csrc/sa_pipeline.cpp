@@ -238,6 +238,23 @@ struct KVSource {
   int64_t sk_t, sk_h, sv_t, sv_h;  // element strides, used when on_device
 };
 
+// Joins the side stream back into the compute stream when a split span ends,
+// including an early return on error, so that nothing enqueued later on the
+// compute stream can overlap the second half's launches.
+struct SideJoin {
+  sa_pipeline* p;
+  hipStream_t compute;
+  bool active = false;
+  int32_t finish() {
+    if (!active) return 0;
+    active = false;
+    SA_HIP_RETURN(hipEventRecord(p->join, p->side));
+    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->join, 0));
+    return 0;
+  }
+  ~SideJoin() { (void)finish(); }
+};
+
 // Apply K/V rows [kv_local_offset, kv_local_offset + kv_tokens) of one segment
 // to the resident Q block, kv_chunk_tokens rows per launch.  `initialize` is
 // true while the state still has to be defined by the next launch; it is
@@ -265,9 +282,11 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
   const int32_t split = (!src.on_device && q_tokens >= 512) ? (q_tokens / 2 + 255) / 256 * 256 : q_tokens;
   const bool two = split < q_tokens && kv_tokens > 0;
   const char* q_second = static_cast<const char*>(q) + (int64_t)split * sq_t * 2;
+  SideJoin join{p, compute};
   if (two) {
     SA_HIP_RETURN(hipEventRecord(p->fork, compute));
     SA_HIP_RETURN(hipStreamWaitEvent(p->side, p->fork, 0));
+    join.active = true;
   }
   for (int32_t start = 0; start < kv_tokens; start += p->kv_chunk) {
     const int64_t position = (int64_t)kv_local_offset + start;
@@ -315,11 +334,7 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
     }
     *initialize = false;
   }
-  if (two) {
-    SA_HIP_RETURN(hipEventRecord(p->join, p->side));
-    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->join, 0));
-  }
-  return 0;
+  return join.finish();
 }
 
 // Gathered span: consecutive segment positions [kv_local_offset, +total)
