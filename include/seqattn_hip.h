@@ -325,6 +325,19 @@ int32_t sa_pipeline_run_resident(sa_pipeline* pipeline, const void* q, const voi
                                  void* compute_stream, sa_pipeline_stats* stats);
 
 /*
+ * Attach caller-owned device scratch for sa_pipeline_run_resident (NULL and 0
+ * detach it).  No counterpart in the reference.  With head_dim 128, a fused
+ * resident launch whose segment has kv_tokens keys first copies V into it,
+ * transposed per K/V head ([kv_heads][128][keys padded to a multiple of 64],
+ * 16-bit), when kv_heads * 128 * roundup(kv_tokens, 64) * 2 bytes fit; the
+ * update kernel then reads V^T fragments with half the LDS instructions.
+ * Results are identical with or without it.  The pipeline keeps the pointer
+ * until it is replaced or the pipeline is destroyed; runs on one pipeline
+ * share it, in stream order.
+ */
+int32_t sa_pipeline_attach_resident_scratch(sa_pipeline* pipeline, void* scratch, int64_t bytes);
+
+/*
  * Finalize the resident state on compute_stream (executor.py:125-142).
  * slot >= 0: into output slot `slot`; the Q-free event is recorded first (the
  * next Q H2D may start) and finalize waits for the slot's previous D2H.

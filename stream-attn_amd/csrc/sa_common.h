@@ -69,7 +69,11 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
                       hipStream_t stream, int32_t merge_keys = 0,
-                      const FusedOutput* fused = nullptr);
+                      const FusedOutput* fused = nullptr, bool v_transposed = false);
+// V [kv_tokens, kv_heads, 128] -> vt [kv_heads][128][t_pad] in the key order
+// the update kernel's transposed-V variant reads, zero keys up to t_pad.
+int32_t launch_transpose_v(const void* v, int64_t sv_t, int64_t sv_h, int32_t kv_tokens, int32_t kv_heads,
+                           int32_t head_dim, void* vt, int64_t t_pad, hipStream_t stream);
 int32_t launch_update_int8(const void* q, const void* k, const void* v, const void* k_scales,
                            const void* v_scales, float* m, float* l, float* acc, int64_t sq_t,
                            int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t, int64_t sv_h,

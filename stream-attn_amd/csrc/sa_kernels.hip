@@ -199,9 +199,16 @@ struct Geometry {
   }
 };
 
-template <typename Op, int DP, bool CAUSAL, bool INIT, bool QUANT>
+// VT: V arrives transposed per K/V head, [head_dim = 128 rows][keys], each
+// 16-key group stored in the order of the MFMA's k slots (keys 0-3, 8-11,
+// 4-7, 12-15; see transpose_v_kernel), padded with zero keys to a multiple of
+// 64.  p.sv_t is then the row stride and p.sv_h the head stride, in elements.
+// A lane's V^T fragment is one 16-byte LDS read instead of two transposing
+// 8-byte reads; the MFMA operands, and so the results, are the same.
+template <typename Op, int DP, bool CAUSAL, bool INIT, bool QUANT, bool VT = false>
 __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const UpdateParams p) {
   using Geo = Geometry<DP>;
+  static_assert(!VT || (DP == 128 && !QUANT), "transposed V is read by the 16-bit head_dim 128 kernel only");
   constexpr int QB = Geo::QB;
   constexpr int QC = DP / 16;  // 16-wide d slices of the QK^T contraction
   constexpr int DB = DP / 32;  // 32-row d blocks of the PV output
@@ -320,12 +327,19 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
     dma_row[i] = row;
     k_off[i] = row * (int)p.sk_t + col;
     v_off[i] = row * (int)p.sv_t + col;
+    if constexpr (VT) {
+      // V^T tile: 128 rows of 64 keys (8 granules of 16 bytes); a 1 KB DMA
+      // moves 8 rows.  LDS granule g of row r holds key granule g ^ vswz(r).
+      const int vrow = chunk * 8 + lane / 8;
+      v_off[i] = vrow * (int)p.sv_t + (((lane % 8) ^ ((vrow >> 1) & 7)) * 8);
+    }
   }
   auto issue_tile = [&](int kt, uint8_t* stage) {
     uint8_t* k_stage = stage;
     uint8_t* v_stage = stage + Geo::TILE_BYTES;
     const uint16_t* kt_base = kp + (int64_t)kt * p.sk_t;
-    const uint16_t* vt_base = vp + (int64_t)kt * p.sv_t;
+    // Transposed V is padded with zero keys to whole tiles: no clamping.
+    const uint16_t* vt_base = VT ? vp + kt : vp + (int64_t)kt * p.sv_t;
     const bool tail = kt + Geo::TILE_KEYS > p.kv_tokens;
 #pragma unroll
     for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
@@ -334,7 +348,7 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
       if (tail && kt + dma_row[i] >= p.kv_tokens) {
         const int back = kt + dma_row[i] - (p.kv_tokens - 1);  // rows to step back
         ko -= back * (int)p.sk_t;
-        vo -= back * (int)p.sv_t;
+        if constexpr (!VT) vo -= back * (int)p.sv_t;
       }
       __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kt_base + ko),
                                        (SA_LDS void*)(k_stage + chunk * 1024), 16, 0, 0);
@@ -455,17 +469,31 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
         u32x4 vf[VB][2];
 #pragma unroll
         for (int dd = 0; dd < VB; ++dd) {
-          const int granule = 4 * (d0 + dd) + 2 * (grp & 1) + ((gi & 3) >> 1);
+          if constexpr (VT) {
+            // Row d = 32 (d0 + dd) + lr, k slots 8 hf .. 8 hf + 7 of the
+            // 16-key group rb / 16 + kc: one granule.
+            const int vrow = 32 * (d0 + dd) + lr;
 #pragma unroll
-          for (int kc = 0; kc < 2; ++kc) {
+            for (int kc = 0; kc < 2; ++kc) {
+              const int g = rb / 8 + 2 * kc + hf;
+              const uint32_t addr = v_lds + vrow * 128 + ((g ^ ((vrow >> 1) & 7)) << 4);
+              u32x4 w;
+              asm volatile("ds_read_b128 %0, %1" : "=v"(w) : "v"(addr));
+              vf[dd][kc] = w;
+            }
+          } else {
+            const int granule = 4 * (d0 + dd) + 2 * (grp & 1) + ((gi & 3) >> 1);
 #pragma unroll
-            for (int r = 0; r < 2; ++r) {
-              const int row = rb + 16 * kc + 8 * r + 4 * (grp >> 1) + (gi >> 2);
-              const uint32_t addr = v_lds + Geo::offset(row, granule) + 8 * (gi & 1);
-              u32x2 w;
-              asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(addr));
-              vf[dd][kc][2 * r] = w[0];
-              vf[dd][kc][2 * r + 1] = w[1];
+            for (int kc = 0; kc < 2; ++kc) {
+#pragma unroll
+              for (int r = 0; r < 2; ++r) {
+                const int row = rb + 16 * kc + 8 * r + 4 * (grp >> 1) + (gi >> 2);
+                const uint32_t addr = v_lds + Geo::offset(row, granule) + 8 * (gi & 1);
+                u32x2 w;
+                asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(addr));
+                vf[dd][kc][2 * r] = w[0];
+                vf[dd][kc][2 * r + 1] = w[1];
+              }
             }
           }
         }
@@ -720,13 +748,71 @@ __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
   }
 }
 
-template <typename Op, int DP, bool QUANT>
+// Transposed copy of V for the VT update kernel.  V is [kv_tokens, kv_heads,
+// 128] with element strides (sv_t, sv_h); vt is [kv_heads][128][t_pad].  Key
+// k of a 16-key group goes to slot k with bits 2 and 3 swapped (slots 0-7
+// hold keys 0-3 and 8-11, slots 8-15 keys 4-7 and 12-15): the k-slot order in
+// which the update kernel's P^T operand holds the keys of a 32x32x16 MFMA, as
+// laid out by the S^T accumulator rows.  Keys kv_tokens .. t_pad-1 are zero.
+// One workgroup per (kv_head, 64 keys), staged through LDS.
+struct TransposeParams {
+  const uint16_t* v;
+  uint16_t* vt;
+  int64_t sv_t, sv_h, t_pad;
+  int32_t kv_tokens, tiles;
+};
+
+__global__ __launch_bounds__(256) void transpose_v_kernel(const TransposeParams p) {
+  __shared__ __attribute__((aligned(16))) uint16_t tile[64][128 + 8];
+  const int tid = threadIdx.x;
+  const int head = blockIdx.x / p.tiles;
+  const int kt = (blockIdx.x - head * p.tiles) * 64;
+  {
+    // Thread t reads key kt + t / 4, elements 32 (t % 4) .. +31.
+    const int key = tid >> 2, d0 = (tid & 3) * 32;
+    const bool ok = kt + key < p.kv_tokens;
+    const uint16_t* src = p.v + (int64_t)(kt + key) * p.sv_t + (int64_t)head * p.sv_h + d0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const u32x4 w = ok ? *reinterpret_cast<const u32x4*>(src + 8 * j) : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(&tile[key][d0 + 8 * j]) = w;
+    }
+  }
+  __syncthreads();
+  {
+    // Thread t writes row d = t / 2, slots 32 (t % 2) .. +31.
+    const int d = tid >> 1, s0 = (tid & 1) * 32;
+    uint16_t* dst = p.vt + ((int64_t)head * 128 + d) * p.t_pad + kt + s0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int sa = s0 + 8 * j + 2 * e, sb = sa + 1;
+        const int ka = (sa & ~12) | ((sa & 4) << 1) | ((sa & 8) >> 1);
+        const int kb = (sb & ~12) | ((sb & 4) << 1) | ((sb & 8) >> 1);
+        w[e] = (uint32_t)tile[ka][d] | ((uint32_t)tile[kb][d] << 16);
+      }
+      *reinterpret_cast<u32x4*>(dst + 8 * j) = w;
+    }
+  }
+}
+
+template <typename Op, int DP, bool QUANT, bool VT = false>
 hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t s) {
   using Geo = Geometry<DP>;
   p.q_blocks = (p.q_tokens + Geo::BLOCK_M - 1) / Geo::BLOCK_M;
   const int64_t total = (int64_t)p.q_blocks * p.q_heads;
   p.xcd_run = (int32_t)((total + 7) / 8);
   const dim3 grid((unsigned)(8 * (int64_t)p.xcd_run));
+  if constexpr (VT) {
+    // Transposed V serves launches that start the state (checked by the caller).
+    if (causal)
+      hipLaunchKernelGGL((update_kernel<Op, DP, true, true, QUANT, true>), grid, dim3(Geo::THREADS), 0, s, p);
+    else
+      hipLaunchKernelGGL((update_kernel<Op, DP, false, true, QUANT, true>), grid, dim3(Geo::THREADS), 0, s, p);
+    return hipGetLastError();
+  }
   if (causal) {
     if (init)
       hipLaunchKernelGGL((update_kernel<Op, DP, true, true, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
@@ -774,7 +860,8 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t q_tokens, int32_t kv_tokens, int32_t q_heads, int32_t kv_heads,
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
-                      hipStream_t stream, int32_t merge_keys, const FusedOutput* fused) {
+                      hipStream_t stream, int32_t merge_keys, const FusedOutput* fused,
+                      bool v_transposed) {
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
     set_error("sa_update_attention_state: unsupported dtype code %d", dtype);
     return SA_ERR_UNSUPPORTED_DTYPE;
@@ -858,6 +945,17 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
   p.q_heads = q_heads;
   const bool causal = (flags & SA_FLAG_CAUSAL) != 0;
   const bool init = (flags & SA_FLAG_INITIALIZE) != 0;
+  if (v_transposed) {
+    // v is transpose_v_kernel's layout: row stride sv_t (keys padded to whole
+    // 64-key tiles), head stride sv_h.
+    if (head_dim != 128 || !init || sv_t % 64 != 0 || sv_t < kv_tokens || sv_h < 128 * sv_t) {
+      set_error("transposed V needs head_dim 128, an initializing launch and a padded [heads][128][keys] layout");
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    hipError_t err = dtype == SA_DTYPE_BF16 ? launch_update_dp<BF16, 128, false, true>(p, causal, init, stream)
+                                            : launch_update_dp<FP16, 128, false, true>(p, causal, init, stream);
+    return err == hipSuccess ? 0 : hip_status(err, "update kernel launch");
+  }
   hipError_t err = dtype == SA_DTYPE_BF16 ? launch_update_op<BF16>(p, dp, causal, init, stream)
                                           : launch_update_op<FP16>(p, dp, causal, init, stream);
   return err == hipSuccess ? 0 : hip_status(err, "update kernel launch");
@@ -946,6 +1044,29 @@ int32_t launch_update_int8(const void* q, const void* k, const void* v, const vo
   hipError_t err = dtype == SA_DTYPE_BF16 ? launch_update_int8_op<BF16>(p, dp, causal, init, stream)
                                           : launch_update_int8_op<FP16>(p, dp, causal, init, stream);
   return err == hipSuccess ? 0 : hip_status(err, "int8 update kernel launch");
+}
+
+int32_t launch_transpose_v(const void* v, int64_t sv_t, int64_t sv_h, int32_t kv_tokens, int32_t kv_heads,
+                           int32_t head_dim, void* vt, int64_t t_pad, hipStream_t stream) {
+  if (head_dim != 128 || kv_tokens < 0 || kv_heads <= 0 || t_pad % 64 != 0 || t_pad < kv_tokens ||
+      t_pad >= (1 << 24) || !v || !vt || sv_t % 8 != 0 || sv_h % 8 != 0 || !aligned(v, 16) ||
+      !aligned(vt, 16)) {
+    set_error("transpose of V: bad arguments (head_dim %d, kv_tokens %d, kv_heads %d, padded keys %lld)",
+              head_dim, kv_tokens, kv_heads, (long long)t_pad);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (t_pad == 0) return 0;
+  TransposeParams p;
+  p.v = static_cast<const uint16_t*>(v);
+  p.vt = static_cast<uint16_t*>(vt);
+  p.sv_t = sv_t;
+  p.sv_h = sv_h;
+  p.t_pad = t_pad;
+  p.kv_tokens = kv_tokens;
+  p.tiles = (int32_t)(t_pad / 64);
+  hipLaunchKernelGGL(transpose_v_kernel, dim3((unsigned)((int64_t)kv_heads * p.tiles)), dim3(256), 0, stream, p);
+  const hipError_t err = hipGetLastError();
+  return err == hipSuccess ? 0 : hip_status(err, "transpose of V");
 }
 
 int32_t launch_finalize(const float* acc, const float* m, const float* l, void* out, float* lse,

@@ -92,6 +92,10 @@ struct sa_pipeline {
   hipEvent_t kv_free_side[3] = {};
   hipEvent_t fork = nullptr, join = nullptr;
   bool kv_side_pending[3] = {false, false, false};
+  // Caller-owned device scratch for a transposed copy of V in HBM-resident
+  // runs (sa_pipeline_attach_resident_scratch); null when none is attached.
+  void* vt_scratch = nullptr;
+  int64_t vt_scratch_bytes = 0;
   hipEvent_t out_ready[2] = {}, out_free[2] = {};
   // sa_pipeline_run with one output slot: the Q block buffer and the output
   // slot take turns as a pass's Q block and output (ready: Q copied in;
@@ -179,7 +183,8 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
                      int32_t q_tokens, int32_t kv_tokens, int32_t q_local_offset,
                      int32_t kv_local_offset, int32_t causal_shift, double scale, int32_t flags,
                      hipStream_t compute, int32_t merge_keys = 0,
-                     const sa::FusedOutput* fused = nullptr, int32_t state_row = 0) {
+                     const sa::FusedOutput* fused = nullptr, int32_t state_row = 0,
+                     bool v_transposed = false) {
   if (p->timing) {
     if (p->t_used == p->t_start.size()) {
       hipEvent_t a = nullptr, b = nullptr;
@@ -196,7 +201,8 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
                                  sq_h, sk_t, sk_h, sv_t, sv_h,
                                  p->q_heads, 1, qt, p->head_dim, q_tokens, kv_tokens, p->q_heads,
                                  p->kv_heads, p->head_dim, q_local_offset, kv_local_offset,
-                                 causal_shift, scale, flags, p->dtype, compute, merge_keys, fused);
+                                 causal_shift, scale, flags, p->dtype, compute, merge_keys, fused,
+                                 v_transposed);
   if (rc != 0) return rc;
   if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
   return 0;
@@ -920,11 +926,24 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
       // per-launch tails and no finalize launches.  Stats count the Q blocks
       // and chunks of the chunked schedule.
       const sa::FusedOutput fused{seg_out, stride_ot, stride_oh, lse, lse_stride_h, q_start};
-      int32_t rc = launch_timed(p, qd + q_start * stride_qt * 2, stride_qt, stride_qh, src.k, src.sk_t,
-                                src.sk_h, src.v, src.sv_t, src.sv_h, (int32_t)q_length, (int32_t)k_length, 0,
-                                0, causal_shift, softmax_scale,
-                                (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, p->kv_chunk,
-                                &fused);
+      // With head_dim 128 and enough attached scratch, V is first copied
+      // transposed (keys padded to whole tiles), which the update kernel
+      // reads with half the LDS instructions for the same operands.
+      const int64_t t_pad = (k_length + 63) / 64 * 64;
+      const int64_t vt_bytes = (int64_t)p->kv_heads * 128 * t_pad * 2;
+      const bool vt = p->head_dim == 128 && p->vt_scratch != nullptr && vt_bytes <= p->vt_scratch_bytes &&
+                      t_pad < (1 << 24);
+      int32_t rc = 0;
+      if (vt) {
+        rc = sa::launch_transpose_v(src.v, src.sv_t, src.sv_h, (int32_t)k_length, p->kv_heads, p->head_dim,
+                                    p->vt_scratch, t_pad, compute);
+        if (rc != 0) return rc;
+      }
+      rc = launch_timed(p, qd + q_start * stride_qt * 2, stride_qt, stride_qh, src.k, src.sk_t, src.sk_h,
+                        vt ? static_cast<const char*>(p->vt_scratch) : src.v, vt ? t_pad : src.sv_t,
+                        vt ? 128 * t_pad : src.sv_h, (int32_t)q_length, (int32_t)k_length, 0, 0, causal_shift,
+                        softmax_scale, (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, p->kv_chunk,
+                        &fused, 0, vt);
       if (rc != 0) return rc;
       const int64_t block = pass_rows(q_length, p->q_chunk);
       for (int64_t qs = q_start; qs < q_stop; qs += block) {
@@ -1014,6 +1033,18 @@ int32_t sa_pipeline_synchronize(sa_pipeline* p) {
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
+  return 0;
+}
+
+int32_t sa_pipeline_attach_resident_scratch(sa_pipeline* p, void* scratch, int64_t bytes) {
+  sa::clear_error();
+  if (!p || bytes < 0 || (scratch == nullptr) != (bytes == 0) ||
+      (scratch && reinterpret_cast<uintptr_t>(scratch) % 16 != 0)) {
+    sa::set_error("sa_pipeline_attach_resident_scratch: need a 16-byte aligned buffer and its size, or NULL and 0");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  p->vt_scratch = scratch;
+  p->vt_scratch_bytes = bytes;
   return 0;
 }
 

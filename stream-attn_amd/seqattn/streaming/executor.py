@@ -101,6 +101,8 @@ class HipExecutorMixin:
         workspace = self._workspace
         self._check_lse(lse, q.shape[0])
         native_stats = _native.PipelineStats()
+        with torch.cuda.device(self.plan.device):
+            workspace.attach_resident_scratch(max((b - a for a, b in zip(k_bounds[:-1], k_bounds[1:])), default=0))
         with torch.cuda.device(self.plan.device), self._range("seqattn:run_resident"):
             status = _native.lib().sa_pipeline_run_resident(
                 workspace.handle,

@@ -86,6 +86,30 @@ class CudaWorkspace:
         _native.check(status, "sa_pipeline_create")
         self._lib = lib
         self.handle = handle
+        self.plan = plan
+        self.resident_scratch: torch.Tensor | None = None
+
+    def attach_resident_scratch(self, kv_tokens: int) -> None:
+        """HBM-resident runs with head_dim 128: device scratch for V
+        transposed per K/V head, [kv_heads, 128, kv_tokens padded to a
+        multiple of 64] 16-bit elements, which the update kernel reads with
+        half the LDS instructions.  Grown on demand and kept for later runs;
+        outside the planner's workspace budget, like the resident inputs."""
+        plan = self.plan
+        if plan.head_dim != 128 or kv_tokens <= 0:
+            return
+        needed = plan.kv_heads * 128 * ((kv_tokens + 63) // 64 * 64) * 2
+        if self.resident_scratch is None or self.resident_scratch.numel() < needed:
+            # Allocated on the compute stream, where every run that reads it is
+            # enqueued, so the caching allocator reuses a dropped buffer only
+            # after those runs.
+            self.resident_scratch = None
+            with torch.cuda.stream(self.compute_stream):
+                self.resident_scratch = torch.empty(needed, dtype=torch.uint8, device=self.device)
+            status = self._lib.sa_pipeline_attach_resident_scratch(
+                self.handle, self.resident_scratch.data_ptr(), self.resident_scratch.numel()
+            )
+            _native.check(status, "sa_pipeline_attach_resident_scratch")
 
     def close(self) -> None:
         handle = getattr(self, "handle", None)

@@ -202,10 +202,11 @@ def test_device_resident_inputs_are_bit_identical_to_streamed(causal, kv_chunk):
 ])
 def test_fused_resident_launch_matches_streamed_at_every_geometry(dtype, head_dim, q_heads, kv_heads):
     """With device inputs and a K/V chunk that is a multiple of 64, each
-    segment is one launch that finalizes its rows in the epilogue.  At every
-    kernel geometry and both 16-bit dtypes it gives the pinned-host streamed
-    run's output and LSE bit for bit, causal, including the first segment's
-    200 queries that see no key (output 0, LSE -inf)."""
+    segment is one launch that finalizes its rows in the epilogue (at head_dim
+    128 reading a transposed copy of V, keys padded with zeros to whole
+    tiles).  At every kernel geometry and both 16-bit dtypes it gives the
+    pinned-host streamed run's output and LSE bit for bit, causal, including
+    the first segment's 200 queries that see no key (output 0, LSE -inf)."""
     announce(f"fused resident launch {dtype} d={head_dim} heads={q_heads}/{kv_heads}")
     gen = torch.Generator().manual_seed(41)
     q = pinned_randn((700, q_heads, head_dim), dtype, gen)
@@ -220,6 +221,8 @@ def test_fused_resident_launch_matches_streamed_at_every_geometry(dtype, head_di
     torch.testing.assert_close(out_d.cpu(), out, atol=0, rtol=0)
     torch.testing.assert_close(lse_d.cpu(), lse, atol=0, rtol=0)
     assert torch.isneginf(lse_d[:, :200]).all() and (out_d[:200] == 0).all()
+    # head_dim 128 reads V through the transposed copy in the attached scratch.
+    assert (runner._workspace.resident_scratch is not None) == (head_dim == 128)
     ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=192, kv_chunk=128, causal=True)
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
