@@ -56,6 +56,13 @@ def test_argument_errors_surface_without_a_gpu():
             None, None, None, None, None, *([0] * 8), 4, 4, 12, 0, None), "finalize")
 
 
+@pytest.mark.skipif(not _native.library_is_built(), reason="native library not built")
+def test_resident_scratch_attach_rejects_bad_arguments_without_a_gpu():
+    lib = _native.lib()
+    assert lib.sa_pipeline_attach_resident_scratch(None, None, 0) == -1
+    assert b"sa_pipeline_attach_resident_scratch" in lib.sa_last_error()
+
+
 def test_backend_resolution_never_falls_back_to_cpu():
     with pytest.raises(ValueError, match="not part of this package"):
         resolve_backend("reference", torch.bfloat16, torch.device("cpu"))
