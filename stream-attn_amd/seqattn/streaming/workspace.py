@@ -116,6 +116,7 @@ class CudaWorkspace:
         if handle is not None and handle.value:
             self._lib.sa_pipeline_destroy(handle)
             self.handle = None
+        self.resident_scratch = None
 
     def __del__(self) -> None:
         try:
