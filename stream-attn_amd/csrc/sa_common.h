@@ -22,24 +22,28 @@ int32_t hip_status(hipError_t err, const char* what);
 
 // Makes `device` current for the lifetime of the guard and restores the
 // caller's device afterwards (torch tracks its own current device per thread).
+// status() reports a failure to query or select the device; callers return
+// it before enqueueing anything.
 class DeviceGuard {
  public:
   explicit DeviceGuard(int device) {
-    hipGetDevice(&previous_);
-    if (previous_ != device) {
-      hipSetDevice(device);
-      changed_ = true;
+    status_ = hipGetDevice(&previous_);
+    if (status_ == hipSuccess && previous_ != device) {
+      status_ = hipSetDevice(device);
+      changed_ = status_ == hipSuccess;
     }
   }
   ~DeviceGuard() {
-    if (changed_) hipSetDevice(previous_);
+    if (changed_) (void)hipSetDevice(previous_);  // nothing to report from a destructor
   }
+  hipError_t status() const { return status_; }
   DeviceGuard(const DeviceGuard&) = delete;
   DeviceGuard& operator=(const DeviceGuard&) = delete;
 
  private:
   int previous_ = 0;
   bool changed_ = false;
+  hipError_t status_ = hipSuccess;
 };
 
 }  // namespace sa

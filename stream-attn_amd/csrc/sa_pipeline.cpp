@@ -124,32 +124,33 @@ void add_stats(sa_pipeline_stats* st, int64_t h2d, int64_t d2h, int64_t qc, int6
   st->max_resident_q_tokens = std::max(st->max_resident_q_tokens, resident);
 }
 
+// Teardown: failures here cannot be acted on, so their codes are dropped.
 void release(sa_pipeline* p) {
-  if (p->h2d) hipStreamSynchronize(p->h2d);
-  if (p->d2h) hipStreamSynchronize(p->d2h);
-  if (p->side) hipStreamSynchronize(p->side);
+  if (p->h2d) (void)hipStreamSynchronize(p->h2d);
+  if (p->d2h) (void)hipStreamSynchronize(p->d2h);
+  if (p->side) (void)hipStreamSynchronize(p->side);
   hipEvent_t* evs[] = {&p->q_ready, &p->q_free, &p->fork, &p->join};
   for (hipEvent_t* e : evs)
-    if (*e) hipEventDestroy(*e);
+    if (*e) (void)hipEventDestroy(*e);
   for (int i = 0; i < 3; ++i) {
-    if (p->kv_ready[i]) hipEventDestroy(p->kv_ready[i]);
-    if (p->kv_free[i]) hipEventDestroy(p->kv_free[i]);
-    if (p->kv_free_side[i]) hipEventDestroy(p->kv_free_side[i]);
+    if (p->kv_ready[i]) (void)hipEventDestroy(p->kv_ready[i]);
+    if (p->kv_free[i]) (void)hipEventDestroy(p->kv_free[i]);
+    if (p->kv_free_side[i]) (void)hipEventDestroy(p->kv_free_side[i]);
   }
   for (int i = 0; i < 2; ++i) {
-    if (p->out_ready[i]) hipEventDestroy(p->out_ready[i]);
-    if (p->out_free[i]) hipEventDestroy(p->out_free[i]);
-    if (p->alt_ready[i]) hipEventDestroy(p->alt_ready[i]);
-    if (p->alt_done[i]) hipEventDestroy(p->alt_done[i]);
-    if (p->alt_free[i]) hipEventDestroy(p->alt_free[i]);
+    if (p->out_ready[i]) (void)hipEventDestroy(p->out_ready[i]);
+    if (p->out_free[i]) (void)hipEventDestroy(p->out_free[i]);
+    if (p->alt_ready[i]) (void)hipEventDestroy(p->alt_ready[i]);
+    if (p->alt_done[i]) (void)hipEventDestroy(p->alt_done[i]);
+    if (p->alt_free[i]) (void)hipEventDestroy(p->alt_free[i]);
   }
-  for (hipEvent_t e : p->t_start) hipEventDestroy(e);
-  for (hipEvent_t e : p->t_stop) hipEventDestroy(e);
+  for (hipEvent_t e : p->t_start) (void)hipEventDestroy(e);
+  for (hipEvent_t e : p->t_stop) (void)hipEventDestroy(e);
   if (p->owns_streams) {
-    if (p->h2d) hipStreamDestroy(p->h2d);
-    if (p->d2h) hipStreamDestroy(p->d2h);
+    if (p->h2d) (void)hipStreamDestroy(p->h2d);
+    if (p->d2h) (void)hipStreamDestroy(p->d2h);
   }
-  if (p->side) hipStreamDestroy(p->side);
+  if (p->side) (void)hipStreamDestroy(p->side);
 }
 
 // Make the H2D stream wait until ring slot `slot` is no longer read by any
@@ -703,7 +704,11 @@ int32_t sa_pipeline_create(sa_pipeline** out_pipeline, int32_t device, void* q_b
   p->kv_row_bytes = (int64_t)kv_heads * head_dim * 2;
 
   sa::DeviceGuard guard(device);
-  hipError_t err = hipSuccess;
+  hipError_t err = guard.status();
+  if (err != hipSuccess) {
+    delete p;
+    return sa::hip_status(err, "sa_pipeline_create: selecting the device");
+  }
   if ((h2d_stream == nullptr) != (d2h_stream == nullptr)) {
     delete p;
     sa::set_error("sa_pipeline_create: pass both copy streams or neither");
@@ -763,6 +768,7 @@ int32_t sa_pipeline_load_q(sa_pipeline* p, const void* q_host, int32_t q_tokens,
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   return load_q(p, q_host, q_tokens, static_cast<hipStream_t>(compute_stream), stats);
 }
 
@@ -773,6 +779,7 @@ int32_t sa_pipeline_stream_kv(sa_pipeline* p, const void* k_host, const void* v_
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   return stream_kv(p, k_host, v_host, k_length, q_tokens, q_local_offset, causal_shift,
                    softmax_scale, causal, static_cast<hipStream_t>(compute_stream), stats);
 }
@@ -789,6 +796,7 @@ int32_t sa_pipeline_stream_kv_span(sa_pipeline* p, const void* k_host, const voi
     return SA_ERR_INVALID_ARGUMENT;
   }
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
   const int64_t qt = (int64_t)p->q_heads * p->head_dim;
   KVSource src{static_cast<const char*>(k_host), static_cast<const char*>(v_host), false, 0, 0, 0, 0};
@@ -821,6 +829,7 @@ int32_t sa_pipeline_stream_kv_gather(sa_pipeline* p, const void* const* k_fragme
     return SA_ERR_INVALID_ARGUMENT;
   }
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
   bool init = *initialize != 0;
   int32_t rc = apply_gather(p, k_fragments, v_fragments, nullptr, nullptr, fragment_tokens,
@@ -872,6 +881,7 @@ int32_t sa_pipeline_stream_kv_gather_int8(
     return SA_ERR_INVALID_ARGUMENT;
   }
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
   bool init = *initialize != 0;
   static const void* const kNoFragment = nullptr;
@@ -898,6 +908,7 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
     return SA_ERR_INVALID_ARGUMENT;
   }
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
   const char* qd = static_cast<const char*>(q);
   const char* kd = static_cast<const char*>(k);
@@ -985,6 +996,7 @@ int32_t sa_pipeline_finalize(sa_pipeline* p, int32_t slot, int32_t q_tokens, flo
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   return finalize(p, slot, q_tokens, lse, lse_stride_h, lse_token_offset,
                   static_cast<hipStream_t>(compute_stream));
 }
@@ -1000,6 +1012,7 @@ int32_t sa_pipeline_finalize_into(sa_pipeline* p, void* dest, int64_t stride_ot,
     return SA_ERR_INVALID_ARGUMENT;
   }
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
   SA_HIP_RETURN(hipEventRecord(p->q_free, compute));
   p->q_pending = true;
@@ -1013,6 +1026,7 @@ int32_t sa_pipeline_release_q(sa_pipeline* p, void* compute_stream) {
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   SA_HIP_RETURN(hipEventRecord(p->q_free, static_cast<hipStream_t>(compute_stream)));
   p->q_pending = true;
   return 0;
@@ -1024,6 +1038,7 @@ int32_t sa_pipeline_d2h(sa_pipeline* p, void* dst_host, const void* src, int64_t
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   return d2h(p, dst_host, src, bytes, event_slot, release_q,
              static_cast<hipStream_t>(compute_stream), stats);
 }
@@ -1032,6 +1047,7 @@ int32_t sa_pipeline_synchronize(sa_pipeline* p) {
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
   return 0;
 }
@@ -1060,6 +1076,7 @@ int32_t sa_pipeline_kernel_timing(sa_pipeline* p, double* total_ms, int64_t* lau
   sa::clear_error();
   if (!p || !total_ms || !launches) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   double total = 0.0;
   for (size_t i = 0; i < p->t_used; ++i) {
     SA_HIP_RETURN(hipEventSynchronize(p->t_stop[i]));
@@ -1097,6 +1114,7 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
     return SA_ERR_INVALID_ARGUMENT;
   }
   sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
   const char* qh = static_cast<const char*>(q_host);
   const char* kh = static_cast<const char*>(k_host);
