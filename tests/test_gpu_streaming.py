@@ -227,6 +227,30 @@ def test_fused_resident_launch_matches_streamed_at_every_geometry(dtype, head_di
     check(out_d.cpu(), lse_d, ref_o, ref_l)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_transposed_v_pads_short_segments_exactly(causal):
+    """The HBM-resident head_dim-128 launch reads V through a copy padded with
+    zero keys to whole 64-key tiles.  Segments of 3 keys, none, exactly one
+    tile and one key past a tile give the streamed run's output and LSE bit
+    for bit."""
+    announce(f"transposed V short segments causal={causal}")
+    gen = torch.Generator().manual_seed(47)
+    cu_q = torch.tensor([0, 5, 5, 75, 76], dtype=torch.int32)
+    cu_k = torch.tensor([0, 3, 3, 67, 196], dtype=torch.int32)
+    q = pinned_randn((76, 4, 128), torch.bfloat16, gen)
+    k = pinned_randn((196, 2, 128), torch.bfloat16, gen)
+    v = pinned_randn((196, 2, 128), torch.bfloat16, gen)
+    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=64, kv_chunk_tokens=64)
+    out, lse, runner = run(q, k, v, cu_q, cu_k, config, causal=causal)
+    out_d, lse_d = runner(q.cuda(), k.cuda(), v.cuda(), cu_q, cu_k, causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert runner._workspace.resident_scratch is not None
+    torch.testing.assert_close(out_d.cpu(), out, atol=0, rtol=0)
+    torch.testing.assert_close(lse_d.cpu(), lse, atol=0, rtol=0)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=64, kv_chunk=64, causal=causal)
+    check(out_d.cpu(), lse_d, ref_o, ref_l)
+
+
 @pytest.mark.parametrize("num_kv", [1, 3])
 @pytest.mark.parametrize("causal", [False, True])
 def test_split_chunk_updates_on_two_streams_are_bit_identical(causal, num_kv):
