@@ -380,11 +380,18 @@ int32_t sa_pipeline_synchronize(sa_pipeline* pipeline);
 /*
  * Kernel timing of the update launches: with enable != 0, every later update
  * launch of the pipeline is bracketed by a pair of timing events on the
- * compute stream.  sa_pipeline_kernel_timing waits for the recorded launches,
- * returns their summed duration (ms) and count, and resets the record.
+ * stream it is launched on (the compute stream, or the pipeline's second
+ * stream for the concurrent half of a split chunk update).
+ * sa_pipeline_kernel_timing waits for the recorded launches, returns their
+ * summed duration (ms) and count, and resets the record.
+ * sa_pipeline_kernel_busy does the same and also returns the length of the
+ * union of the launch intervals (ms): the time at least one update launch
+ * was running, in which overlapping half-launches count once.
  */
 int32_t sa_pipeline_set_kernel_timing(sa_pipeline* pipeline, int32_t enable);
 int32_t sa_pipeline_kernel_timing(sa_pipeline* pipeline, double* total_ms, int64_t* launches);
+int32_t sa_pipeline_kernel_busy(sa_pipeline* pipeline, double* busy_ms, double* total_ms,
+                                int64_t* launches);
 
 /* hipStream_t of the pipeline's H2D (which == 0) or D2H (which == 1) copy stream. */
 void* sa_pipeline_stream(sa_pipeline* pipeline, int32_t which);

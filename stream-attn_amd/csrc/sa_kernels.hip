@@ -41,6 +41,10 @@
 // logits exceeds m + 8; otherwise p = exp2(s*scale - m) <= 2^8 against the
 // kept m.  The decision is per query, so results do not depend on how queries
 // are grouped into wavefronts or Q blocks.
+// Each step first computes P against the kept m and tests the lane's partial
+// row sum: every p <= 2^8 whenever that sum is, so the row maximum (and its
+// cross-lane exchange) is only taken on the rare steps that may rescale, and
+// the result is the same as deciding on the maximum.
 // (m, l, acc) remains an exact representation of the partial softmax:
 // out = acc / l and LSE = m + log2(l) are unchanged, and P keeps bf16's
 // relative precision.  The row sum l is accumulated per lane half and the two
@@ -405,40 +409,10 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
         }
       }
 
-      // Half-row maxima (this lane's 16 keys) in the scaled domain.
-      float mx[QB];
-      bool grow = false;
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        float a = fmaxf(fmaxf(s[qb][0], s[qb][1]), s[qb][2]);
-#pragma unroll
-        for (int i = 3; i < 15; i += 2) a = fmaxf(fmaxf(a, s[qb][i]), s[qb][i + 1]);
-        a = fmaxf(a, s[qb][15]);
-        mx[qb] = a * cf;
-        grow = grow || (mx[qb] > m_run[qb] + kRescaleThreshold);
-      }
-      // Rescale only when some logit of the wave left the [.., m + 8] window.
-      // Inside the branch each query still decides for itself (both lane
-      // halves of a query see the same decision), so a query's result never
-      // depends on which other queries share its wavefront.
-      if (__ballot(grow) != 0) {
-#pragma unroll
-        for (int qb = 0; qb < QB; ++qb) {
-          const float full = fmaxf(mx[qb], __shfl_xor(mx[qb], 32));
-          const float m_new = full > m_run[qb] + kRescaleThreshold ? full : m_run[qb];
-          const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run[qb] - m_new);
-          l_part[qb] *= alpha;
-#pragma unroll
-          for (int d = 0; d < DB; ++d) acc[qb][d] *= alpha;
-          m_run[qb] = m_new;
-        }
-      }
-
-      // P^T (B operands of PV) and the partial row sums.
-      u32x4 pf[QB][2];
-#pragma unroll
-      for (int qb = 0; qb < QB; ++qb) {
-        const float neg_m = m_run[qb] == -INFINITY ? 0.f : -m_run[qb];
+      // P^T (B operands of PV) and this lane's partial row sums, first against
+      // the kept maximum m: p = exp2(s * scale - m).  The pairwise sum order
+      // is fixed, so a row's sum does not depend on which path computed it.
+      auto exps = [&](int qb, float neg_m, u32x4 (&pq)[2]) -> float {
         float sum = 0.f;
 #pragma unroll
         for (int kc = 0; kc < 2; ++kc) {
@@ -446,12 +420,49 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
           for (int e = 0; e < 4; ++e) {
             const float p0 = __builtin_amdgcn_exp2f(fmaf(s[qb][8 * kc + 2 * e], cf, neg_m));
             const float p1 = __builtin_amdgcn_exp2f(fmaf(s[qb][8 * kc + 2 * e + 1], cf, neg_m));
-            sum += p0 + p1;
-            pf[qb][kc][e] = Op::pack2(p0, p1);
+            sum = (kc == 0 && e == 0) ? p0 + p1 : sum + (p0 + p1);
+            pq[kc][e] = Op::pack2(p0, p1);
           }
         }
-        l_part[qb] += sum;
+        return sum;
+      };
+      u32x4 pf[QB][2];
+      float psum[QB];
+      bool grow = false;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        psum[qb] = exps(qb, m_run[qb] == -INFINITY ? 0.f : -m_run[qb], pf[qb]);
+        // Every p <= 2^8 (no logit above m + 8) whenever the lane's sum is;
+        // a row without a maximum yet always takes the rescale path.
+        grow = grow || !(psum[qb] <= 256.f) || m_run[qb] == -INFINITY;
       }
+      // Rescale only when some logit of the wave may have left the [.., m + 8]
+      // window.  The rule is that of the half-row maxima: m moves to the
+      // query's full maximum when that exceeds m + 8.  Each query decides
+      // for itself (both lane halves of a query see the same decision), so a
+      // query's result never depends on which other queries share its
+      // wavefront; where m stays, the values computed above stand.
+      if (__ballot(grow) != 0) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          float a = fmaxf(fmaxf(s[qb][0], s[qb][1]), s[qb][2]);
+#pragma unroll
+          for (int i = 3; i < 15; i += 2) a = fmaxf(fmaxf(a, s[qb][i]), s[qb][i + 1]);
+          a = fmaxf(a, s[qb][15]) * cf;
+          const float full = fmaxf(a, __shfl_xor(a, 32));
+          const float m_new = full > m_run[qb] + kRescaleThreshold ? full : m_run[qb];
+          if (m_new != m_run[qb]) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+            l_part[qb] *= alpha;
+#pragma unroll
+            for (int d = 0; d < DB; ++d) acc[qb][d] *= alpha;
+            m_run[qb] = m_new;
+            psum[qb] = exps(qb, -m_new, pf[qb]);
+          }
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) l_part[qb] += psum[qb];
 
       // O^T += V^T P^T; each V^T fragment (two transposing LDS reads) feeds QB
       // MFMAs.  The reads of a batch of up to 4 d-blocks are all issued before

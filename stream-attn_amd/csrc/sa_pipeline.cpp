@@ -34,6 +34,7 @@
 #include <cstring>
 #include <functional>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "sa_common.h"
@@ -1072,22 +1073,46 @@ int32_t sa_pipeline_set_kernel_timing(sa_pipeline* p, int32_t enable) {
   return 0;
 }
 
-int32_t sa_pipeline_kernel_timing(sa_pipeline* p, double* total_ms, int64_t* launches) {
+int32_t sa_pipeline_kernel_busy(sa_pipeline* p, double* busy_ms, double* total_ms, int64_t* launches) {
   sa::clear_error();
-  if (!p || !total_ms || !launches) return SA_ERR_INVALID_ARGUMENT;
+  if (!p || !busy_ms || !total_ms || !launches) return SA_ERR_INVALID_ARGUMENT;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
+  // Launch intervals as offsets from the first recorded start; the events of
+  // both streams share the device's clock.
+  std::vector<std::pair<double, double>> spans;
+  spans.reserve(p->t_used);
   double total = 0.0;
   for (size_t i = 0; i < p->t_used; ++i) {
     SA_HIP_RETURN(hipEventSynchronize(p->t_stop[i]));
-    float ms = 0.f;
-    SA_HIP_RETURN(hipEventElapsedTime(&ms, p->t_start[i], p->t_stop[i]));
-    total += ms;
+    float begin = 0.f, end = 0.f;
+    SA_HIP_RETURN(hipEventElapsedTime(&begin, p->t_start[0], p->t_start[i]));
+    SA_HIP_RETURN(hipEventElapsedTime(&end, p->t_start[0], p->t_stop[i]));
+    spans.emplace_back(begin, end);
+    total += end - begin;
   }
+  std::sort(spans.begin(), spans.end());
+  double busy = 0.0, open_begin = 0.0, open_end = -1.0;
+  for (const auto& s : spans) {
+    if (open_end < open_begin || s.first > open_end) {
+      if (open_end >= open_begin) busy += open_end - open_begin;
+      open_begin = s.first;
+      open_end = s.second;
+    } else {
+      open_end = std::max(open_end, s.second);
+    }
+  }
+  if (!spans.empty()) busy += open_end - open_begin;
+  *busy_ms = busy;
   *total_ms = total;
   *launches = (int64_t)p->t_used;
   p->t_used = 0;
   return 0;
+}
+
+int32_t sa_pipeline_kernel_timing(sa_pipeline* p, double* total_ms, int64_t* launches) {
+  double busy = 0.0;
+  return sa_pipeline_kernel_busy(p, &busy, total_ms, launches);
 }
 
 void* sa_pipeline_stream(sa_pipeline* p, int32_t which) {

@@ -128,6 +128,9 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "sa_pipeline_kernel_timing": (
         c_int32, [c_void_p, ctypes.POINTER(c_double), ctypes.POINTER(c_int64)]
     ),
+    "sa_pipeline_kernel_busy": (
+        c_int32, [c_void_p, ctypes.POINTER(c_double), ctypes.POINTER(c_double), ctypes.POINTER(c_int64)]
+    ),
     "sa_pipeline_stream": (c_void_p, [c_void_p, c_int32]),
     "sa_pipeline_output_slot": (c_void_p, [c_void_p, c_int32]),
     "sa_pipeline_q_buffer": (c_void_p, [c_void_p]),

@@ -49,10 +49,18 @@ class StreamingAttentionConfig:
     require_pinned: bool = True
     pin_output: bool = True
     enable_nvtx: bool = False
+    # HBM-resident inputs with head_dim 128 read V through a transposed copy
+    # in device scratch (kv_heads * 128 * kv_tokens * 2 bytes, outside the
+    # workspace budget).  None: no cap; 0: never; otherwise the largest
+    # scratch the runner may allocate.  Without it V is read in place, with
+    # bit-identical results.
+    resident_scratch_limit_bytes: int | None = None
 
     def validate(self) -> None:
         if self.workspace_budget_bytes is not None and self.workspace_budget_bytes <= 0:
             raise ValueError("workspace_budget_bytes must be positive")
+        if self.resident_scratch_limit_bytes is not None and self.resident_scratch_limit_bytes < 0:
+            raise ValueError("resident_scratch_limit_bytes must be non-negative")
         if self.q_chunk_tokens is not None and self.q_chunk_tokens <= 0:
             raise ValueError("q_chunk_tokens must be positive")
         if self.kv_chunk_tokens is not None and self.kv_chunk_tokens <= 0:

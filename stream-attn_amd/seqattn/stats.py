@@ -17,6 +17,9 @@ class StreamingAttentionStats:
     q_chunk_tokens: int = 0
     kv_chunk_tokens: int = 0
     max_resident_q_tokens: int = 0
+    # Device scratch of the transposed V used by the last HBM-resident run
+    # (0: V was read in place).  Not a reference field.
+    resident_scratch_bytes: int = 0
 
     def as_dict(self) -> dict[str, int | float | str]:
         return asdict(self)

@@ -96,13 +96,23 @@ class HipExecutorMixin:
         """HBM-resident inputs and output: one native call, no PCIe traffic.
 
         Enqueued on the runner's compute stream (torch's current stream at
-        construction); the caller synchronizes as with any torch op.
+        construction), ordered after the work the caller's current stream has
+        enqueued so far, and the caller's stream waits for it in turn: the
+        inputs may come from, and the output go to, work on any stream, and the
+        caller synchronizes as with any torch op.
         """
         workspace = self._workspace
         self._check_lse(lse, q.shape[0])
         native_stats = _native.PipelineStats()
+        compute = workspace.compute_stream
         with torch.cuda.device(self.plan.device):
-            workspace.attach_resident_scratch(max((b - a for a, b in zip(k_bounds[:-1], k_bounds[1:])), default=0))
+            caller = torch.cuda.current_stream()
+            longest_k = max((b - a for a, b in zip(k_bounds[:-1], k_bounds[1:])), default=0)
+            stats.resident_scratch_bytes = workspace.attach_resident_scratch(
+                longest_k, self.config.resident_scratch_limit_bytes
+            )
+            if caller != compute:
+                compute.wait_stream(caller)
         with torch.cuda.device(self.plan.device), self._range("seqattn:run_resident"):
             status = _native.lib().sa_pipeline_run_resident(
                 workspace.handle,
@@ -112,9 +122,11 @@ class HipExecutorMixin:
                 out.stride(0), out.stride(1), 0 if lse is None else lse.stride(0),
                 _bounds_array(q_bounds), _bounds_array(k_bounds), len(q_bounds) - 1,
                 float(scale), int(bool(causal)),
-                workspace.compute_stream.cuda_stream, ctypes.byref(native_stats),
+                compute.cuda_stream, ctypes.byref(native_stats),
             )
         _native.check(status, "sa_pipeline_run_resident")
+        if caller != compute:
+            caller.wait_stream(compute)
         _merge_stats(stats, native_stats)
         return out
 

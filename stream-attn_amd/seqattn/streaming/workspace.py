@@ -12,7 +12,9 @@ current stream at creation.
 
 from __future__ import annotations
 
+import atexit
 import ctypes
+import weakref
 
 import torch
 
@@ -21,6 +23,28 @@ from ..planner import AttentionPlan
 
 
 _COPY_STREAMS: dict[int, tuple[torch.cuda.Stream, torch.cuda.Stream]] = {}
+# Every workspace with a live native pipeline, so that all of them can be
+# destroyed while the HIP runtime is still up (see close_all_workspaces).
+_LIVE: "weakref.WeakSet[CudaWorkspace]" = weakref.WeakSet()
+
+
+def close_all_workspaces() -> None:
+    """Destroy every live pipeline and drop the shared copy streams.
+
+    Registered with ``atexit``: it runs before the interpreter tears down
+    modules and before the shared libraries' static destructors, so no
+    pipeline (its events and side stream) and no scratch buffer is released
+    after the HIP runtime has begun to shut down.
+    """
+    for workspace in list(_LIVE):
+        try:
+            workspace.close()
+        except Exception:  # noqa: BLE001 - best effort at shutdown
+            pass
+    _COPY_STREAMS.clear()
+
+
+atexit.register(close_all_workspaces)
 
 
 def copy_streams(device: torch.device) -> tuple[torch.cuda.Stream, torch.cuda.Stream]:
@@ -88,35 +112,63 @@ class CudaWorkspace:
         self.handle = handle
         self.plan = plan
         self.resident_scratch: torch.Tensor | None = None
+        _LIVE.add(self)
 
-    def attach_resident_scratch(self, kv_tokens: int) -> None:
+    def _attach(self, buffer: torch.Tensor | None) -> None:
+        status = self._lib.sa_pipeline_attach_resident_scratch(
+            self.handle, None if buffer is None else buffer.data_ptr(), 0 if buffer is None else buffer.numel()
+        )
+        _native.check(status, "sa_pipeline_attach_resident_scratch")
+
+    def attach_resident_scratch(self, kv_tokens: int, limit_bytes: int | None = None) -> int:
         """HBM-resident runs with head_dim 128: device scratch for V
         transposed per K/V head, [kv_heads, 128, kv_tokens padded to a
         multiple of 64] 16-bit elements, which the update kernel reads with
         half the LDS instructions.  Grown on demand and kept for later runs;
-        outside the planner's workspace budget, like the resident inputs."""
+        outside the planner's workspace budget, like the resident inputs.
+
+        Returns the scratch bytes the next run will use, 0 when it reads V in
+        place instead: ``limit_bytes`` caps the scratch (0 disables it), and
+        an allocation that fails for lack of device memory also leaves the
+        run on the in-place path, which gives the same results bit for bit.
+        """
         plan = self.plan
         if plan.head_dim != 128 or kv_tokens <= 0:
-            return
+            return 0
         needed = plan.kv_heads * 128 * ((kv_tokens + 63) // 64 * 64) * 2
-        if self.resident_scratch is None or self.resident_scratch.numel() < needed:
+        if self.resident_scratch is not None and self.resident_scratch.numel() >= needed:
+            return needed
+        if limit_bytes is not None and needed > limit_bytes:
+            return 0
+        # The pipeline must not hold the old buffer's address once it is dropped.
+        if self.resident_scratch is not None:
+            self._attach(None)
+            self.resident_scratch = None
+        try:
             # Allocated on the compute stream, where every run that reads it is
             # enqueued, so the caching allocator reuses a dropped buffer only
             # after those runs.
-            self.resident_scratch = None
             with torch.cuda.stream(self.compute_stream):
-                self.resident_scratch = torch.empty(needed, dtype=torch.uint8, device=self.device)
-            status = self._lib.sa_pipeline_attach_resident_scratch(
-                self.handle, self.resident_scratch.data_ptr(), self.resident_scratch.numel()
-            )
-            _native.check(status, "sa_pipeline_attach_resident_scratch")
+                scratch = torch.empty(needed, dtype=torch.uint8, device=self.device)
+        except torch.cuda.OutOfMemoryError:
+            return 0
+        self._attach(scratch)
+        self.resident_scratch = scratch
+        return needed
 
     def close(self) -> None:
         handle = getattr(self, "handle", None)
         if handle is not None and handle.value:
+            # Work already enqueued on the compute stream records this
+            # pipeline's events and reads its scratch: let it finish first.
+            try:
+                self.compute_stream.synchronize()
+            except RuntimeError:
+                pass
             self._lib.sa_pipeline_destroy(handle)
             self.handle = None
         self.resident_scratch = None
+        _LIVE.discard(self)
 
     def __del__(self) -> None:
         try:
@@ -125,4 +177,4 @@ class CudaWorkspace:
             pass
 
 
-__all__ = ["CudaWorkspace", "copy_streams"]
+__all__ = ["CudaWorkspace", "close_all_workspaces", "copy_streams"]
