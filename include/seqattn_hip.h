@@ -389,6 +389,17 @@ int32_t sa_pipeline_synchronize(sa_pipeline* pipeline);
  * was running, in which overlapping half-launches count once.
  */
 int32_t sa_pipeline_set_kernel_timing(sa_pipeline* pipeline, int32_t enable);
+
+/*
+ * Host-side trace ranges: with enable != 0 the pipeline brackets the enqueue
+ * of each stage with ROCm tracer (roctx) ranges named like the reference's
+ * NVTX ranges (streaming/executor.py:53-174, enabled there by
+ * config.enable_nvtx): "seqattn:q_h2d", "seqattn:kv_h2d",
+ * "seqattn:fused_update", "seqattn:fused_finalize", "seqattn:output_d2h".
+ * The tracer library is loaded on first use; SA_ERR_BAD_STATE when it is
+ * missing.
+ */
+int32_t sa_pipeline_set_trace_ranges(sa_pipeline* pipeline, int32_t enable);
 int32_t sa_pipeline_kernel_timing(sa_pipeline* pipeline, double* total_ms, int64_t* launches);
 int32_t sa_pipeline_kernel_busy(sa_pipeline* pipeline, double* busy_ms, double* total_ms,
                                 int64_t* launches);

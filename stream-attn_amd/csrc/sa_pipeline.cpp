@@ -24,6 +24,7 @@
 // workgroups overlaps the other's work instead of leaving CUs idle.  Every
 // row's arithmetic is that of a single launch: results are bit-identical.
 
+#include <dlfcn.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -63,6 +64,52 @@ int32_t hip_status(hipError_t err, const char* what) {
 }
 
 }  // namespace sa
+
+namespace {
+
+// Host-side trace ranges named like the reference's NVTX ranges
+// (streaming/executor.py: seqattn:q_h2d, kv_h2d, fused_update,
+// fused_finalize, output_d2h), bracketing the enqueue of each stage.  The
+// ROCm tracer API is resolved with dlopen when ranges are first enabled, so
+// the library has no link-time dependency on it.
+struct TraceApi {
+  int (*push)(const char*) = nullptr;
+  int (*pop)() = nullptr;
+};
+
+const TraceApi& trace_api() {
+  static const TraceApi api = [] {
+    TraceApi a;
+    for (const char* name : {"librocprofiler-sdk-roctx.so.1", "librocprofiler-sdk-roctx.so", "libroctx64.so.4",
+                             "libroctx64.so"}) {
+      void* handle = dlopen(name, RTLD_NOW | RTLD_LOCAL);
+      if (!handle) continue;
+      a.push = reinterpret_cast<int (*)(const char*)>(dlsym(handle, "roctxRangePushA"));
+      a.pop = reinterpret_cast<int (*)()>(dlsym(handle, "roctxRangePop"));
+      if (a.push && a.pop) break;
+      a = TraceApi();
+    }
+    return a;
+  }();
+  return api;
+}
+
+class TraceRange {
+ public:
+  TraceRange(bool enabled, const char* name) : on_(enabled && trace_api().push) {
+    if (on_) trace_api().push(name);
+  }
+  ~TraceRange() {
+    if (on_) trace_api().pop();
+  }
+  TraceRange(const TraceRange&) = delete;
+  TraceRange& operator=(const TraceRange&) = delete;
+
+ private:
+  bool on_;
+};
+
+}  // namespace
 
 struct sa_pipeline {
   int device = 0;
@@ -107,6 +154,8 @@ struct sa_pipeline {
   bool out_pending[2] = {false, false};
   int64_t ring_next = 0;  // next K/V ring slot (rotates across calls)
 
+  // Host-side trace ranges around each stage's enqueue (sa_pipeline_set_trace_ranges).
+  bool trace = false;
   // Optional timing of update launches (event pairs on the compute stream).
   bool timing = false;
   std::vector<hipEvent_t> t_start, t_stop;
@@ -168,6 +217,7 @@ int32_t load_q(sa_pipeline* p, const void* q_host, int32_t q_tokens, hipStream_t
     sa::set_error("q_tokens %d outside [0, q_chunk_tokens=%d]", q_tokens, p->q_chunk);
     return SA_ERR_INVALID_ARGUMENT;
   }
+  TraceRange range(p->trace, "seqattn:q_h2d");
   const int64_t bytes = (int64_t)q_tokens * p->q_row_bytes;
   if (p->q_pending) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->q_free, 0));
   if (bytes > 0)
@@ -187,6 +237,7 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
                      hipStream_t compute, int32_t merge_keys = 0,
                      const sa::FusedOutput* fused = nullptr, int32_t state_row = 0,
                      bool v_transposed = false) {
+  TraceRange range(p->trace, "seqattn:fused_update");
   if (p->timing) {
     if (p->t_used == p->t_start.size()) {
       hipEvent_t a = nullptr, b = nullptr;
@@ -215,6 +266,7 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
 int32_t launch_timed_int8(sa_pipeline* p, int slot, int32_t q_tokens, int32_t kv_tokens,
                           int32_t q_local_offset, int32_t kv_local_offset, int32_t causal_shift,
                           double scale, int32_t flags, hipStream_t compute) {
+  TraceRange range(p->trace, "seqattn:fused_update");
   if (p->timing) {
     if (p->t_used == p->t_start.size()) {
       hipEvent_t a = nullptr, b = nullptr;
@@ -311,13 +363,16 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
     } else {
       const int slot = (int)(p->ring_next++ % p->num_kv);
       const int64_t bytes = (int64_t)n * p->kv_row_bytes;
-      int32_t wrc = wait_slot_free(p, slot);
-      if (wrc != 0) return wrc;
-      SA_HIP_RETURN(hipMemcpyAsync(p->k_slots[slot], src.k + (int64_t)start * p->kv_row_bytes,
-                                   bytes, hipMemcpyHostToDevice, p->h2d));
-      SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], src.v + (int64_t)start * p->kv_row_bytes,
-                                   bytes, hipMemcpyHostToDevice, p->h2d));
-      SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
+      {
+        TraceRange range(p->trace, "seqattn:kv_h2d");
+        int32_t wrc = wait_slot_free(p, slot);
+        if (wrc != 0) return wrc;
+        SA_HIP_RETURN(hipMemcpyAsync(p->k_slots[slot], src.k + (int64_t)start * p->kv_row_bytes,
+                                     bytes, hipMemcpyHostToDevice, p->h2d));
+        SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], src.v + (int64_t)start * p->kv_row_bytes,
+                                     bytes, hipMemcpyHostToDevice, p->h2d));
+        SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
+      }
       add_stats(st, 2 * bytes, 0, 0, 1, 0);
       if (after_copy) {
         const int32_t hrc = (*after_copy)(start / p->kv_chunk);
@@ -393,39 +448,42 @@ int32_t apply_gather(sa_pipeline* p, const void* const* k_frags, const void* con
     if (!*initialize && position >= visible_end) break;
     const int32_t n = (int32_t)std::min<int64_t>(p->kv_chunk, total - start);
     const int slot = (int)(p->ring_next++ % p->num_kv);
-    int32_t wrc = wait_slot_free(p, slot);
-    if (wrc != 0) return wrc;
     char* kd = static_cast<char*>(p->k_slots[slot]);
     char* vd = static_cast<char*>(p->v_slots[slot]);
-    int64_t filled = 0;
-    while (filled < n) {
-      while (frag < nfrag && frag_row >= frag_tokens[frag]) {
-        ++frag;
-        frag_row = 0;
-      }
-      const int64_t rows = std::min<int64_t>(n - filled, frag_tokens[frag] - frag_row);
-      const int64_t bytes = rows * row_bytes;
-      const int64_t src_off = frag_row * row_bytes;
-      SA_HIP_RETURN(hipMemcpyAsync(kd + filled * row_bytes,
-                                   static_cast<const char*>(k_frags[frag]) + src_off, bytes,
-                                   hipMemcpyHostToDevice, p->h2d));
-      SA_HIP_RETURN(hipMemcpyAsync(vd + filled * row_bytes,
-                                   static_cast<const char*>(v_frags[frag]) + src_off, bytes,
-                                   hipMemcpyHostToDevice, p->h2d));
-      if (int8) {
-        const int64_t sbytes = rows * scale_row_bytes;
-        const int64_t ssrc = frag_row * scale_row_bytes;
-        SA_HIP_RETURN(hipMemcpyAsync(static_cast<char*>(p->ks_slots[slot]) + filled * scale_row_bytes,
-                                     static_cast<const char*>(ks_frags[frag]) + ssrc, sbytes,
+    {
+      TraceRange kv_range(p->trace, "seqattn:kv_h2d");
+      int32_t wrc = wait_slot_free(p, slot);
+      if (wrc != 0) return wrc;
+      int64_t filled = 0;
+      while (filled < n) {
+        while (frag < nfrag && frag_row >= frag_tokens[frag]) {
+          ++frag;
+          frag_row = 0;
+        }
+        const int64_t rows = std::min<int64_t>(n - filled, frag_tokens[frag] - frag_row);
+        const int64_t bytes = rows * row_bytes;
+        const int64_t src_off = frag_row * row_bytes;
+        SA_HIP_RETURN(hipMemcpyAsync(kd + filled * row_bytes,
+                                     static_cast<const char*>(k_frags[frag]) + src_off, bytes,
                                      hipMemcpyHostToDevice, p->h2d));
-        SA_HIP_RETURN(hipMemcpyAsync(static_cast<char*>(p->vs_slots[slot]) + filled * scale_row_bytes,
-                                     static_cast<const char*>(vs_frags[frag]) + ssrc, sbytes,
+        SA_HIP_RETURN(hipMemcpyAsync(vd + filled * row_bytes,
+                                     static_cast<const char*>(v_frags[frag]) + src_off, bytes,
                                      hipMemcpyHostToDevice, p->h2d));
+        if (int8) {
+          const int64_t sbytes = rows * scale_row_bytes;
+          const int64_t ssrc = frag_row * scale_row_bytes;
+          SA_HIP_RETURN(hipMemcpyAsync(static_cast<char*>(p->ks_slots[slot]) + filled * scale_row_bytes,
+                                       static_cast<const char*>(ks_frags[frag]) + ssrc, sbytes,
+                                       hipMemcpyHostToDevice, p->h2d));
+          SA_HIP_RETURN(hipMemcpyAsync(static_cast<char*>(p->vs_slots[slot]) + filled * scale_row_bytes,
+                                       static_cast<const char*>(vs_frags[frag]) + ssrc, sbytes,
+                                       hipMemcpyHostToDevice, p->h2d));
+        }
+        filled += rows;
+        frag_row += rows;
       }
-      filled += rows;
-      frag_row += rows;
+      SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
     }
-    SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
     add_stats(st, 2 * (int64_t)n * (row_bytes + (int8 ? scale_row_bytes : 0)), 0, 0, 1, 0);
     SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
     const int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (*initialize ? SA_FLAG_INITIALIZE : 0);
@@ -477,6 +535,7 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
 
 int32_t finalize(sa_pipeline* p, int32_t slot, int32_t q_tokens, float* lse, int64_t lse_sh,
                  int64_t lse_off, hipStream_t compute) {
+  TraceRange range(p->trace, "seqattn:fused_finalize");
   void* dest;
   if (slot >= 0) {
     if (!p->has_out_slots || slot >= p->num_out) {
@@ -503,6 +562,7 @@ int32_t d2h(sa_pipeline* p, void* dst, const void* src, int64_t bytes, int32_t s
     sa::set_error("event slot %d outside [0, %d)", slot, p->num_out);
     return SA_ERR_INVALID_ARGUMENT;
   }
+  TraceRange range(p->trace, "seqattn:output_d2h");
   SA_HIP_RETURN(hipEventRecord(p->out_ready[slot], compute));
   SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->out_ready[slot], 0));
   if (bytes > 0) SA_HIP_RETURN(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, p->d2h));
@@ -558,6 +618,7 @@ int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const ch
   auto copy_piece = [&](size_t i, int j) -> int32_t {
     const Pass& ps = passes[i];
     const int b = (int)(i & 1);
+    TraceRange range(p->trace, "seqattn:q_h2d");
     if (j == 0 && pending[b]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->alt_free[b], 0));
     const int64_t r0 = (int64_t)ps.n * j / kPieces, r1 = (int64_t)ps.n * (j + 1) / kPieces;
     const int64_t bytes = (r1 - r0) * p->q_row_bytes;
@@ -609,15 +670,21 @@ int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const ch
     if (rc) return rc;
     while (has_next && next_piece < kPieces)
       if ((rc = copy_piece(i + 1, next_piece++)) != 0) return rc;
-    rc = sa::launch_finalize(p->acc, p->m, p->l, buf[b], lse, q_stride, p->head_dim, p->q_heads, 1, q_stride,
-                             p->head_dim, lse_sh, ps.qt, ps.n, p->q_heads, p->head_dim, p->dtype, compute);
-    if (rc) return rc;
-    SA_HIP_RETURN(hipEventRecord(p->alt_done[b], compute));
-    SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->alt_done[b], 0));
+    {
+      TraceRange range(p->trace, "seqattn:fused_finalize");
+      rc = sa::launch_finalize(p->acc, p->m, p->l, buf[b], lse, q_stride, p->head_dim, p->q_heads, 1, q_stride,
+                               p->head_dim, lse_sh, ps.qt, ps.n, p->q_heads, p->head_dim, p->dtype, compute);
+      if (rc) return rc;
+      SA_HIP_RETURN(hipEventRecord(p->alt_done[b], compute));
+    }
     const int64_t bytes = (int64_t)ps.n * p->q_row_bytes;
-    if (bytes > 0)
-      SA_HIP_RETURN(hipMemcpyAsync(oh + ps.qt * p->q_row_bytes, buf[b], bytes, hipMemcpyDeviceToHost, p->d2h));
-    SA_HIP_RETURN(hipEventRecord(p->alt_free[b], p->d2h));
+    {
+      TraceRange range(p->trace, "seqattn:output_d2h");
+      SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->alt_done[b], 0));
+      if (bytes > 0)
+        SA_HIP_RETURN(hipMemcpyAsync(oh + ps.qt * p->q_row_bytes, buf[b], bytes, hipMemcpyDeviceToHost, p->d2h));
+      SA_HIP_RETURN(hipEventRecord(p->alt_free[b], p->d2h));
+    }
     pending[b] = true;
     add_stats(st, 0, bytes, 0, 0, 0);
   }
@@ -1015,6 +1082,7 @@ int32_t sa_pipeline_finalize_into(sa_pipeline* p, void* dest, int64_t stride_ot,
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  TraceRange range(p->trace, "seqattn:fused_finalize");
   SA_HIP_RETURN(hipEventRecord(p->q_free, compute));
   p->q_pending = true;
   const int64_t qt = (int64_t)p->q_heads * p->head_dim;
@@ -1062,6 +1130,17 @@ int32_t sa_pipeline_attach_resident_scratch(sa_pipeline* p, void* scratch, int64
   }
   p->vt_scratch = scratch;
   p->vt_scratch_bytes = bytes;
+  return 0;
+}
+
+int32_t sa_pipeline_set_trace_ranges(sa_pipeline* p, int32_t enable) {
+  sa::clear_error();
+  if (!p) return SA_ERR_INVALID_ARGUMENT;
+  if (enable && !trace_api().push) {
+    sa::set_error("sa_pipeline_set_trace_ranges: no ROCm tracer library (roctx) could be loaded");
+    return SA_ERR_BAD_STATE;
+  }
+  p->trace = enable != 0;
   return 0;
 }
 

@@ -10,7 +10,7 @@ the same kernels and pipeline, and ``ProjectedAttentionRunner`` fuses a
 caller's QKV and output projections around the streamed attention.
 """
 
-from .api import StreamingAttentionRunner, streaming_attn_func, streaming_attn_varlen_func
+from .api import StreamingAttentionRunner, clear_runner_cache, streaming_attn_func, streaming_attn_varlen_func
 from .config import PagedAttentionConfig, ProjectionPipelineConfig, StreamingAttentionConfig
 from .paged import (
     CallbackOutputSink,
@@ -64,6 +64,7 @@ __all__ = [
     "build_plan",
     "ephemeral_nvme_directory",
     "load_nvme_output",
+    "clear_runner_cache",
     "streaming_attn_func",
     "streaming_attn_varlen_func",
     "streaming_projected_self_attention",

@@ -1,6 +1,21 @@
-"""FlashAttention-style entry points (reference src/seqattn_core/api.py:15-113)."""
+"""FlashAttention-style entry points.
+
+Names, signatures, validation messages and results follow the reference
+(src/seqattn_core/api.py:15-113): packed ``[tokens, heads, head_dim]``
+varlen inputs with ``cu_seqlens``, or dense ``[batch, seqlen, heads,
+head_dim]`` inputs, in host DRAM, with the output returned in host DRAM.
+
+What differs is the runner's lifetime.  A runner owns an HBM workspace and a
+native pipeline (streams, events), which costs more to build than a small
+attention call takes to run, so these functions keep the runner of the last
+(plan, config) pair and reuse it while calls repeat it.  A lock serializes
+calls on the shared runner, so concurrent callers stay correct.
+``clear_runner_cache()`` releases it; a different plan replaces it.
+"""
 
 from __future__ import annotations
+
+import threading
 
 import torch
 
@@ -9,9 +24,36 @@ from .planner import AttentionPlan, build_plan
 from .stats import StreamingAttentionStats
 from .streaming import StreamingAttentionRunner
 
+_cache_lock = threading.Lock()
+_cached: tuple[tuple, StreamingAttentionRunner] | None = None
 
-def _max_segment_length(cu_seqlens: torch.Tensor) -> int:
-    return int(torch.diff(cu_seqlens.to(dtype=torch.int64)).max().item())
+
+def clear_runner_cache() -> None:
+    """Release the runner kept by the last API call (its workspace and pipeline)."""
+    global _cached
+    with _cache_lock:
+        if _cached is not None:
+            _cached[1].close()
+            _cached = None
+
+
+def _run_cached(plan: AttentionPlan, config: StreamingAttentionConfig, call):
+    global _cached
+    key = (plan, config)
+    with _cache_lock:
+        if _cached is None or _cached[0] != key:
+            if _cached is not None:
+                _cached[1].close()
+                _cached = None
+            _cached = (key, StreamingAttentionRunner(plan, config))
+        return call(_cached[1])
+
+
+def _longest_segment(cu_seqlens: torch.Tensor) -> int:
+    bounds = cu_seqlens.to(dtype=torch.int64)
+    if bounds.numel() < 2:
+        return 0
+    return int((bounds[1:] - bounds[:-1]).max().item())
 
 
 def streaming_attn_varlen_func(
@@ -40,31 +82,18 @@ def streaming_attn_varlen_func(
     """
     if dropout_p != 0:
         raise ValueError("seqattn V1 is inference-only and requires dropout_p=0")
-    longest_q = _max_segment_length(cu_seqlens_q)
-    longest_k = _max_segment_length(cu_seqlens_k)
-    if max_seqlen_q is not None and longest_q > max_seqlen_q:
-        raise ValueError("cu_seqlens_q exceeds max_seqlen_q")
-    if max_seqlen_k is not None and longest_k > max_seqlen_k:
-        raise ValueError("cu_seqlens_k exceeds max_seqlen_k")
-    config = StreamingAttentionConfig() if config is None else config
+    for cu, limit, which in ((cu_seqlens_q, max_seqlen_q, "q"), (cu_seqlens_k, max_seqlen_k, "k")):
+        if limit is not None and _longest_segment(cu) > limit:
+            raise ValueError(f"cu_seqlens_{which} exceeds max_seqlen_{which}")
+    config = config if config is not None else StreamingAttentionConfig()
     plan = build_plan(
-        q_heads=q.shape[1],
-        kv_heads=k.shape[1],
-        head_dim=q.shape[2],
-        dtype=q.dtype,
-        device=device,
-        max_q_tokens=q.shape[0],
-        max_kv_tokens=k.shape[0],
-        config=config,
+        q_heads=q.shape[1], kv_heads=k.shape[1], head_dim=q.shape[2], dtype=q.dtype, device=device,
+        max_q_tokens=q.shape[0], max_kv_tokens=k.shape[0], config=config,
     )
-    runner = StreamingAttentionRunner(plan, config)
-    try:
-        return runner(
-            q, k, v, cu_seqlens_q, cu_seqlens_k,
-            softmax_scale=softmax_scale, causal=causal, out=out, stats=stats, return_lse=return_lse,
-        )
-    finally:
-        runner.close()
+    return _run_cached(plan, config, lambda runner: runner(
+        q, k, v, cu_seqlens_q, cu_seqlens_k,
+        softmax_scale=softmax_scale, causal=causal, out=out, stats=stats, return_lse=return_lse,
+    ))
 
 
 def streaming_attn_func(
@@ -80,24 +109,26 @@ def streaming_attn_func(
     stats: StreamingAttentionStats | None = None,
     device: torch.device | str = "cuda",
 ) -> torch.Tensor:
-    """Dense batched wrapper over host ``[batch, seqlen, heads, head_dim]`` tensors."""
-    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+    """Dense batched wrapper over host ``[batch, seqlen, heads, head_dim]`` tensors:
+    every batch entry is one segment of the packed varlen call."""
+    if any(t.ndim != 4 for t in (q, k, v)):
         raise ValueError("dense q, k, and v must use [batch, seqlen, heads, head_dim]")
     if q.shape[0] != k.shape[0] or k.shape != v.shape:
         raise ValueError("dense q/k/v batch and k/v shapes must match")
-    batch, q_length, q_heads, head_dim = q.shape
-    k_length, kv_heads = k.shape[1], k.shape[2]
-    q_packed = q.reshape(batch * q_length, q_heads, head_dim)
-    k_packed = k.reshape(batch * k_length, kv_heads, head_dim)
-    v_packed = v.reshape(batch * k_length, kv_heads, head_dim)
-    cu_q = torch.arange(0, (batch + 1) * q_length, q_length, dtype=torch.int32)
-    cu_k = torch.arange(0, (batch + 1) * k_length, k_length, dtype=torch.int32)
-    out_packed = None if out is None else out.reshape_as(q_packed)
+    batch, q_length, k_length = q.shape[0], q.shape[1], k.shape[1]
+    packed = [t.flatten(0, 1) for t in (q, k, v)]
+    segments = torch.arange(batch + 1, dtype=torch.int32)
     result = streaming_attn_varlen_func(
-        q_packed, k_packed, v_packed, cu_q, cu_k, q_length, k_length, dropout_p, softmax_scale, causal,
-        config=config, out=out_packed, stats=stats, device=device,
+        *packed, segments * q_length, segments * k_length, q_length, k_length, dropout_p, softmax_scale, causal,
+        config=config, out=None if out is None else out.flatten(0, 1), stats=stats, device=device,
     )
-    return result.reshape(batch, q_length, q_heads, head_dim)
+    return result.unflatten(0, (batch, q_length))
 
 
-__all__ = ["AttentionPlan", "StreamingAttentionRunner", "streaming_attn_func", "streaming_attn_varlen_func"]
+__all__ = [
+    "AttentionPlan",
+    "StreamingAttentionRunner",
+    "clear_runner_cache",
+    "streaming_attn_func",
+    "streaming_attn_varlen_func",
+]

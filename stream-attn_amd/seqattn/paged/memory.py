@@ -1,16 +1,16 @@
-"""In-memory page sources and sinks (reference src/seqattn_core/paged/memory.py:106-343).
+"""In-memory page sources and sinks.
 
-``MemoryPageSource`` pages caller-owned CPU tensors (which do not count
-toward the operator's host budget); ``MemoryPageSink`` writes output pages
-into a caller-owned CPU tensor; ``CallbackOutputSink`` hands each output page
-to a callback.  Same constructors, validation messages and metrics as the
-reference.
+Same classes, constructors, validation messages and metrics as the
+reference (src/seqattn_core/paged/memory.py:106-343): ``MemoryPageSource``
+pages caller-owned CPU tensors (which do not count toward the operator's
+host budget), ``MemoryPageSink`` writes output pages into a caller-owned CPU
+tensor, ``CallbackOutputSink`` hands each output page to a callback.
 
-Zero-copy: when the caller's tensors are page-locked and stored in their own
-dtype, the paged runner gathers K/V pages straight from them
-(``pinned_kv_rows``) and a ``MemoryPageSink`` over a page-locked tensor
-receives its rows by D2H directly (``pinned_rows``); the reader/writer
-protocol is used otherwise.
+The MI355X runtime prefers not to copy at all: when the caller's tensors are
+page-locked and stored in their own dtype, the paged runner gathers K/V rows
+for the GPU straight from them (``pinned_kv_rows`` / ``pinned_q_rows``) and a
+``MemoryPageSink`` over a page-locked tensor receives its rows by D2H directly
+(``pinned_rows``).  The reader/writer protocol below serves every other case.
 """
 
 from __future__ import annotations
@@ -35,25 +35,62 @@ from .layout import (
 from .memory_budget import HostMemoryPlan
 from .protocols import PageReader, PageSink, PageSource, PageWriter
 
-
-def _zero_tail(out: torch.Tensor, valid: int) -> None:
-    if out.shape[0] > valid:
-        out[valid:].zero_()
+_STORAGE_DTYPES = ("bf16", "fp16", "fp32", "int8")
 
 
-class _MemoryReader(PageReader):
+def _nbytes(tensor: torch.Tensor) -> int:
+    return tensor.numel() * tensor.element_size()
+
+
+def _fill_rows(out: torch.Tensor, rows: torch.Tensor) -> None:
+    """``out[:len(rows)] = rows`` and zeros in the rest of ``out``."""
+    count = rows.shape[0]
+    out[:count].copy_(rows)
+    if out.shape[0] > count:
+        out[count:].zero_()
+
+
+def _timed(started: float, logical: int, quantization: float = 0.0) -> PageReadMetrics:
+    return PageReadMetrics(read_seconds=time.perf_counter() - started, quantization_seconds=quantization,
+                           logical_bytes=logical, physical_bytes=logical)
+
+
+def _check_source_tensors(q, k, v) -> None:
+    if q is None and k is None:
+        raise ValueError("at least one of q or k/v must be supplied")
+    if (k is None) != (v is None):
+        raise ValueError("k and v must be supplied together")
+    for name, tensor in (("q", q), ("k", k), ("v", v)):
+        if tensor is None:
+            continue
+        if tensor.device.type != "cpu" or tensor.ndim != 3 or not tensor.is_contiguous():
+            raise ValueError(f"{name} must be contiguous CPU [tokens, heads, head_dim]")
+    if k is None:
+        return
+    if k.shape != v.shape or k.dtype != v.dtype:
+        raise ValueError("k and v must have matching shape and dtype")
+    if q is not None:
+        if q.shape[2] != k.shape[2] or q.shape[1] % k.shape[1]:
+            raise ValueError("q and k/v head shapes are incompatible")
+        if q.dtype != k.dtype:
+            raise ValueError("q and k/v source dtype must match")
+
+
+class _TensorPageReader(PageReader):
+    """Pages of a ``MemoryPageSource`` copied (or INT8-quantized) into the
+    runtime's page buffers."""
+
     def __init__(self, source: MemoryPageSource) -> None:
         self.source = source
 
     def read_q(self, page: PageDescriptor, out: torch.Tensor) -> PageReadMetrics:
-        if self.source.q is None:
+        q = self.source.q
+        if q is None:
             raise ValueError("this MemoryPageSource has no query tensor")
         started = time.perf_counter()
-        rows = self.source.q[page.token_start : page.token_stop]
-        out[: page.valid_tokens].copy_(rows)
-        _zero_tail(out, page.valid_tokens)
-        size = rows.numel() * rows.element_size()
-        return PageReadMetrics(read_seconds=time.perf_counter() - started, logical_bytes=size, physical_bytes=size)
+        rows = q[page.token_start : page.token_stop]
+        _fill_rows(out, rows)
+        return _timed(started, _nbytes(rows))
 
     def read_kv(
         self,
@@ -63,38 +100,29 @@ class _MemoryReader(PageReader):
         k_scales_out: torch.Tensor | None = None,
         v_scales_out: torch.Tensor | None = None,
     ) -> PageReadMetrics:
-        source = self.source
-        if source.k is None or source.v is None or source.kv_layout is None:
+        src = self.source
+        if src.k is None or src.v is None or src.kv_layout is None:
             raise ValueError("this MemoryPageSource has no K/V tensors")
-        layout = source.kv_layout
+        layout = src.kv_layout
         started = time.perf_counter()
-        k_rows = source.k[page.token_start : page.token_stop]
-        v_rows = source.v[page.token_start : page.token_stop]
+        span = slice(page.token_start, page.token_stop)
         n = page.valid_tokens
-        quant_seconds = 0.0
         logical = 2 * n * layout.storage_bytes_per_token
-        if layout.storage_dtype == "int8":
-            if k_scales_out is None or v_scales_out is None:
-                raise ValueError("INT8 K/V reads require scale buffers")
-            groups = math.ceil(n / layout.quant_group_tokens)
-            quant_started = time.perf_counter()
-            quantize_int8_per_token_group(k_rows, k_out[:n], k_scales_out[:groups],
-                                          group_tokens=layout.quant_group_tokens)
-            quantize_int8_per_token_group(v_rows, v_out[:n], v_scales_out[:groups],
-                                          group_tokens=layout.quant_group_tokens)
-            quant_seconds = time.perf_counter() - quant_started
-            logical += 2 * groups * layout.heads * 2
-        else:
-            k_out[:n].copy_(k_rows)
-            v_out[:n].copy_(v_rows)
-        _zero_tail(k_out, n)
-        _zero_tail(v_out, n)
-        return PageReadMetrics(
-            read_seconds=time.perf_counter() - started,
-            quantization_seconds=quant_seconds,
-            logical_bytes=logical,
-            physical_bytes=logical,
-        )
+        quantization = 0.0
+        if layout.storage_dtype != "int8":
+            _fill_rows(k_out, src.k[span])
+            _fill_rows(v_out, src.v[span])
+            return _timed(started, logical)
+        if k_scales_out is None or v_scales_out is None:
+            raise ValueError("INT8 K/V reads require scale buffers")
+        groups = math.ceil(n / layout.quant_group_tokens)
+        began = time.perf_counter()
+        for rows, codes, scales in ((src.k[span], k_out, k_scales_out), (src.v[span], v_out, v_scales_out)):
+            quantize_int8_per_token_group(rows, codes[:n], scales[:groups], group_tokens=layout.quant_group_tokens)
+            if codes.shape[0] > n:
+                codes[n:].zero_()
+        quantization = time.perf_counter() - began
+        return _timed(started, logical + 2 * groups * layout.heads * 2, quantization)
 
 
 class MemoryPageSource(PageSource):
@@ -116,22 +144,7 @@ class MemoryPageSource(PageSource):
         kv_storage_dtype: str | None = None,
         quant_group_tokens: int = 64,
     ) -> None:
-        if q is None and k is None:
-            raise ValueError("at least one of q or k/v must be supplied")
-        if (k is None) != (v is None):
-            raise ValueError("k and v must be supplied together")
-        for name, tensor in (("q", q), ("k", k), ("v", v)):
-            if tensor is not None and (
-                tensor.device.type != "cpu" or tensor.ndim != 3 or not tensor.is_contiguous()
-            ):
-                raise ValueError(f"{name} must be contiguous CPU [tokens, heads, head_dim]")
-        if k is not None and (k.shape != v.shape or k.dtype != v.dtype):
-            raise ValueError("k and v must have matching shape and dtype")
-        if q is not None and k is not None:
-            if q.shape[2] != k.shape[2] or q.shape[1] % k.shape[1]:
-                raise ValueError("q and k/v head shapes are incompatible")
-            if q.dtype != k.dtype:
-                raise ValueError("q and k/v source dtype must match")
+        _check_source_tensors(q, k, v)
         self.q, self.k, self.v = q, k, v
         self.q_layout: TensorLayout | None = None
         self.kv_layout: KVLayout | None = None
@@ -139,80 +152,71 @@ class MemoryPageSource(PageSource):
         self.kv_pages: tuple[PageDescriptor, ...] = ()
         self.cu_seqlens_q: tuple[int, ...] | None = None
         self.cu_seqlens_k: tuple[int, ...] | None = None
+        paging = {"page_target_bytes": page_target_bytes, "token_alignment": block_n}
         if q is not None:
             if cu_seqlens_q is None:
                 raise ValueError("cu_seqlens_q is required with q")
-            q_bounds = validate_cu_seqlens(cu_seqlens_q, q.shape[0], "cu_seqlens_q")
-            self.cu_seqlens_q = tuple(q_bounds)
+            self.cu_seqlens_q = tuple(validate_cu_seqlens(cu_seqlens_q, q.shape[0], "cu_seqlens_q"))
             self.q_layout = TensorLayout(q.shape[0], q.shape[1], q.shape[2], dtype_name(q.dtype))
-            self.q_pages = build_page_descriptors(
-                q_bounds, bytes_per_token=self.q_layout.bytes_per_token,
-                page_target_bytes=page_target_bytes, token_alignment=block_n,
-            )
+            self.q_pages = build_page_descriptors(self.cu_seqlens_q, bytes_per_token=self.q_layout.bytes_per_token,
+                                                  **paging)
         if k is not None:
             if cu_seqlens_k is None:
                 raise ValueError("cu_seqlens_k is required with k/v")
-            k_bounds = validate_cu_seqlens(cu_seqlens_k, k.shape[0], "cu_seqlens_k")
-            self.cu_seqlens_k = tuple(k_bounds)
-            storage = dtype_name(k.dtype) if kv_storage_dtype is None else kv_storage_dtype
-            if storage not in {"bf16", "fp16", "fp32", "int8"}:
+            self.cu_seqlens_k = tuple(validate_cu_seqlens(cu_seqlens_k, k.shape[0], "cu_seqlens_k"))
+            source_dtype = dtype_name(k.dtype)
+            storage = kv_storage_dtype or source_dtype
+            if storage not in _STORAGE_DTYPES:
                 raise ValueError("unsupported K/V storage dtype")
             if storage != "int8" and torch_dtype(storage) != k.dtype:
                 raise ValueError("exact K/V storage dtype must match the source dtype")
-            self.kv_layout = KVLayout(k.shape[0], k.shape[1], k.shape[2], dtype_name(k.dtype), storage,
-                                      quant_group_tokens)
+            self.kv_layout = KVLayout(k.shape[0], k.shape[1], k.shape[2], source_dtype, storage, quant_group_tokens)
             self.kv_pages = build_page_descriptors(
-                k_bounds, bytes_per_token=self.kv_layout.storage_bytes_per_token,
-                page_target_bytes=page_target_bytes, token_alignment=block_n,
-            )
+                self.cu_seqlens_k, bytes_per_token=self.kv_layout.storage_bytes_per_token, **paging)
 
     def open_reader(self, memory_plan: HostMemoryPlan, queue_depth: int) -> PageReader:
-        del memory_plan, queue_depth
-        return _MemoryReader(self)
+        del memory_plan, queue_depth  # nothing to buffer: rows come from the caller's tensors
+        return _TensorPageReader(self)
 
     def pinned_q_rows(self, start: int, stop: int) -> torch.Tensor | None:
         """Page-locked view of query rows [start, stop), or None."""
-        if self.q is None or not self.q.is_pinned():
-            return None
-        return self.q[start:stop]
+        if self.q is not None and self.q.is_pinned():
+            return self.q[start:stop]
+        return None
 
     def pinned_kv_rows(self, start: int, stop: int) -> tuple[torch.Tensor, torch.Tensor] | None:
         """Page-locked views of K/V rows [start, stop) in storage dtype, or None."""
-        if (
-            self.k is None
-            or self.kv_layout is None
-            or self.kv_layout.storage_dtype != self.kv_layout.source_dtype
-            or not (self.k.is_pinned() and self.v.is_pinned())
-        ):
-            return None
-        return self.k[start:stop], self.v[start:stop]
+        layout = self.kv_layout
+        exact = layout is not None and layout.storage_dtype == layout.source_dtype
+        if exact and self.k.is_pinned() and self.v.is_pinned():
+            return self.k[start:stop], self.v[start:stop]
+        return None
 
 
-class _MemoryPageWriter(PageWriter):
-    def __init__(self, sink: MemoryPageSink, layout: TensorLayout) -> None:
-        self.sink = sink
-        out = sink.out
+class _TensorPageWriter(PageWriter):
+    def __init__(self, out: torch.Tensor | None, layout: TensorLayout) -> None:
         if out is None:
             raise ValueError("MemoryPageSink requires a caller-owned output tensor")
         if tuple(out.shape) != (layout.total_tokens, layout.heads, layout.head_dim):
             raise ValueError("MemoryPageSink output shape does not match the query layout")
         if out.dtype != layout.torch_dtype or out.device.type != "cpu":
             raise ValueError("MemoryPageSink output must be a matching CPU tensor")
+        self.out = out
 
     def write_page(self, page: PageDescriptor, data: torch.Tensor) -> PageReadMetrics:
         started = time.perf_counter()
-        self.sink.out[page.token_start : page.token_stop].copy_(data[: page.valid_tokens])
-        size = page.valid_tokens * data.shape[1] * data.shape[2] * data.element_size()
-        return PageReadMetrics(read_seconds=time.perf_counter() - started, logical_bytes=size, physical_bytes=size)
+        rows = data[: page.valid_tokens]
+        self.out[page.token_start : page.token_stop].copy_(rows)
+        return _timed(started, _nbytes(rows))
 
     def pinned_rows(self, start: int, stop: int) -> torch.Tensor | None:
-        out = self.sink.out
-        if not (out.is_pinned() and out.is_contiguous()):
-            return None
-        return out[start:stop]
+        """Page-locked view of output rows [start, stop) for direct D2H, or None."""
+        if self.out.is_pinned() and self.out.is_contiguous():
+            return self.out[start:stop]
+        return None
 
     def close(self) -> torch.Tensor:
-        return self.sink.out
+        return self.out
 
 
 class MemoryPageSink(PageSink):
@@ -230,7 +234,7 @@ class MemoryPageSink(PageSink):
         queue_depth: int,
     ) -> PageWriter:
         del cu_seqlens, pages, memory_plan, queue_depth
-        return _MemoryPageWriter(self, layout)
+        return _TensorPageWriter(self.out, layout)
 
 
 class _CallbackPageWriter(PageWriter):
@@ -240,10 +244,10 @@ class _CallbackPageWriter(PageWriter):
 
     def write_page(self, page: PageDescriptor, data: torch.Tensor) -> PageReadMetrics:
         started = time.perf_counter()
-        self.callback(page, data[: page.valid_tokens])
+        rows = data[: page.valid_tokens]
+        self.callback(page, rows)
         self.pages_written += 1
-        size = page.valid_tokens * data.shape[1] * data.shape[2] * data.element_size()
-        return PageReadMetrics(read_seconds=time.perf_counter() - started, logical_bytes=size, physical_bytes=size)
+        return _timed(started, _nbytes(rows))
 
     def close(self) -> int:
         return self.pages_written

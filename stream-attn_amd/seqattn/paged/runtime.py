@@ -612,6 +612,8 @@ class _RunState:
         run_plan = replace(plan, q_chunk_tokens=q_rows) if q_rows < plan.q_chunk_tokens else plan
         with torch.cuda.device(device):
             self.workspace = CudaWorkspace(run_plan)
+            if config.attention.enable_nvtx:
+                self.workspace.enable_trace_ranges()
             if self.int8:
                 # One fp16 scale per (row, K/V head) per ring slot, for K and for V.
                 shape = (run_plan.kv_chunk_tokens, run_plan.kv_heads)

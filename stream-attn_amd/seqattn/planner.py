@@ -13,6 +13,16 @@ kv_chunk_tokens and estimated bytes (pinned against the reference README's
 * ``_candidate_cost`` (L158-184): PCIe / state-traffic / launch cost model
   used to pick the K/V chunk jointly with Q.
 
+Measured rates (an addition): ``build_plan(..., rates=PlannerRates(...))``
+scores the same candidates with a model of this pipeline built from rates
+measured on the device (``measure_planner_rates``): per pass, the K/V copies
+of the pass overlap its update launches, so a pass costs the larger of its
+H2D time and its kernel time (FLOP at the measured update rate, FP32 state
+traffic at the HBM rate, a per-launch overhead), and the plan records the
+modeled seconds and the share of the link the plan would use.  Without
+rates the reference's fixed constants decide, so the plans (and the golden
+rows they are pinned to) are unchanged.
+
 gfx950 specifics: on a ROCm device the launch preset is (128, 64, 4, 2) for
 every head_dim: Q chunks align to 128 rows and K/V chunks to the kernel's
 64-key LDS tile (a workgroup covers 256 queries for head_dim <= 128, and
@@ -80,6 +90,16 @@ def _resolve_kernel_config(
 
 
 @dataclass(frozen=True)
+class PlannerRates:
+    """Device rates the planner can decide with (bytes and FLOP per second)."""
+
+    h2d_bytes_per_second: float
+    update_flops_per_second: float
+    hbm_bytes_per_second: float = 5.0e12
+    launch_seconds: float = 8e-6
+
+
+@dataclass(frozen=True)
 class AttentionPlan:
     q_heads: int
     kv_heads: int
@@ -99,6 +119,10 @@ class AttentionPlan:
     num_stages: int
     estimated_workspace_bytes: int
     workspace_budget_bytes: int | None
+    # With measured rates only: modeled seconds of one run over max_q_tokens x
+    # max_kv_tokens, and the share of the measured H2D rate it keeps busy.
+    estimated_seconds: float | None = None
+    h2d_link_fraction: float | None = None
 
     @property
     def group_size(self) -> int:
@@ -200,6 +224,83 @@ def _candidate_cost(
     return kv_stream_bytes * overlap / 24e9 + state_bytes / 1.2e12 + launches * 8e-6
 
 
+def modeled_run(
+    *,
+    q_chunk: int,
+    kv_chunk: int,
+    max_q_tokens: int,
+    max_kv_tokens: int,
+    q_heads: int,
+    kv_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+    rates: PlannerRates,
+) -> tuple[float, float]:
+    """(seconds, H2D link fraction) of one non-causal run of the pipeline.
+
+    Each pass copies its Q block once and streams every K/V chunk; a chunk's
+    copy overlaps the launches of the previous chunk, so a pass takes the
+    larger of its copy time and its kernel time, plus the first chunk's copy,
+    which nothing hides when the pass starts.
+    """
+    element = _element_size(dtype)
+    passes = math.ceil(max_q_tokens / q_chunk)
+    rows = math.ceil(max_q_tokens / passes)
+    chunks = math.ceil(max_kv_tokens / kv_chunk)
+    kv_bytes = 2 * max_kv_tokens * kv_heads * head_dim * element
+    q_bytes = rows * q_heads * head_dim * element
+    h2d_pass = (kv_bytes + q_bytes) / rates.h2d_bytes_per_second
+    flop_pass = 4.0 * q_heads * head_dim * rows * max_kv_tokens
+    state_pass = chunks * 2 * rows * q_heads * (head_dim + 2) * 4
+    kernel_pass = (flop_pass / rates.update_flops_per_second + state_pass / rates.hbm_bytes_per_second
+                   + 2 * chunks * rates.launch_seconds)
+    first_copy = 2 * min(kv_chunk, max_kv_tokens) * kv_heads * head_dim * element / rates.h2d_bytes_per_second
+    seconds = passes * (max(h2d_pass, kernel_pass) + first_copy)
+    return seconds, passes * h2d_pass / seconds
+
+
+def measure_planner_rates(device: torch.device | str = "cuda", *, dtype: torch.dtype = torch.bfloat16,
+                          copy_bytes: int = 512 * 2**20) -> PlannerRates:
+    """Measure the pinned H2D copy rate and the update kernel's rate on
+    ``device`` (a few hundred milliseconds of GPU work)."""
+    import time
+
+    from .kernels import update_attention_state
+
+    device = torch.device(device)
+    src = torch.empty(copy_bytes, dtype=torch.uint8, pin_memory=True)
+    dst = torch.empty(copy_bytes, dtype=torch.uint8, device=device)
+    dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize(device)
+    started = time.perf_counter()
+    for _ in range(3):
+        dst.copy_(src, non_blocking=True)
+    torch.cuda.synchronize(device)
+    h2d = 3 * copy_bytes / (time.perf_counter() - started)
+    del src, dst
+    q_rows, keys, heads, dim = 8192, 4096, 32, 128
+    q = torch.randn((q_rows, heads, dim), device=device).to(dtype)
+    k = torch.randn((keys, heads, dim), device=device).to(dtype)
+    v = torch.randn_like(k)
+    m = torch.empty((q_rows, heads), device=device)
+    l = torch.empty_like(m)
+    acc = torch.empty((q_rows, heads, dim), device=device)
+
+    def launch(initialize):
+        update_attention_state(q, k, v, m, l, acc, q_tokens=q_rows, kv_tokens=keys, q_local_offset=0,
+                               kv_local_offset=0, causal_shift=0, softmax_scale=dim**-0.5, causal=False,
+                               initialize=initialize)
+
+    launch(True)
+    torch.cuda.synchronize(device)
+    started = time.perf_counter()
+    for _ in range(5):
+        launch(False)
+    torch.cuda.synchronize(device)
+    flops = 5 * 4.0 * heads * dim * q_rows * keys / (time.perf_counter() - started)
+    return PlannerRates(h2d_bytes_per_second=h2d, update_flops_per_second=flops)
+
+
 def build_plan(
     *,
     q_heads: int,
@@ -210,8 +311,13 @@ def build_plan(
     max_q_tokens: int,
     max_kv_tokens: int,
     config: StreamingAttentionConfig | None = None,
+    rates: PlannerRates | None = None,
 ) -> AttentionPlan:
-    """Choose (q_chunk_tokens, kv_chunk_tokens) for a shape and budget."""
+    """Choose (q_chunk_tokens, kv_chunk_tokens) for a shape and budget.
+
+    ``rates`` (optional): measured device rates; the candidates are then
+    ranked by the modeled run time of this pipeline instead of the
+    reference's fixed-constant cost."""
     config = StreamingAttentionConfig() if config is None else config
     config.validate()
     device = torch.device(device)
@@ -249,13 +355,12 @@ def build_plan(
                 min(config.block_m, max_q_tokens),
                 _align_down(min(config.q_chunk_tokens, max_q_tokens), config.block_m),
             )
-        cost = _candidate_cost(
-            q_chunk=q_chunk,
-            kv_chunk=kv_chunk,
-            max_q_tokens=max_q_tokens,
-            max_kv_tokens=max_kv_tokens,
-            **shape,
-        )
+        sizes = {"q_chunk": q_chunk, "kv_chunk": kv_chunk, "max_q_tokens": max_q_tokens,
+                 "max_kv_tokens": max_kv_tokens}
+        if rates is None:
+            cost = _candidate_cost(**sizes, **shape)
+        else:
+            cost = modeled_run(**sizes, rates=rates, **shape)[0]
         scored.append((cost, q_chunk, kv_chunk))
 
     if not scored:
@@ -273,6 +378,10 @@ def build_plan(
             f"requested chunks need {estimated / 2**20:.1f} MiB, exceeding the "
             f"{budget / 2**20:.1f} MiB workspace budget"
         )
+    modeled = (None, None)
+    if rates is not None:
+        modeled = modeled_run(q_chunk=q_chunk, kv_chunk=kv_chunk, max_q_tokens=max_q_tokens,
+                              max_kv_tokens=max_kv_tokens, rates=rates, **shape)
     return AttentionPlan(
         q_heads=q_heads,
         kv_heads=kv_heads,
@@ -292,7 +401,16 @@ def build_plan(
         num_stages=config.num_stages,
         estimated_workspace_bytes=estimated,
         workspace_budget_bytes=budget,
+        estimated_seconds=modeled[0],
+        h2d_link_fraction=modeled[1],
     )
 
 
-__all__ = ["AttentionPlan", "build_plan", "estimate_workspace_bytes"]
+__all__ = [
+    "AttentionPlan",
+    "PlannerRates",
+    "build_plan",
+    "estimate_workspace_bytes",
+    "measure_planner_rates",
+    "modeled_run",
+]

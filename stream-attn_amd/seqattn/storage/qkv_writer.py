@@ -1,11 +1,20 @@
-"""Streaming builder of an aligned Q/K/V page store
-(reference src/seqattn_core/storage/qkv_writer.py:26-262).
+"""Builder of the aligned Q/K/V page store.
 
-Pages are written whole (zero padded to their record size) into temporary
-files that are renamed into place and described by a JSON manifest written
-last, atomically; a failed or interrupted build leaves no manifest, so a
-half-written store never opens.  INT8 K/V storage quantizes each page at
-write time.
+Produces the reference's format (src/seqattn_core/storage/qkv_writer.py:26-265
+and storage/records.py): ``q.bin`` and ``kv.bin`` with one 4,096-byte aligned,
+zero-padded record per page, and ``manifest.json`` with the same keys.  The
+construction and error messages are the reference's; the write path is this
+package's own:
+
+* Every record is described as a list of (offset, bytes) pieces.  Buffered
+  files write the pieces straight from the caller's page tensors, with the
+  gaps and the tail filled from one shared zero block, as a single
+  ``pwritev``; O_DIRECT files stage the record in an aligned page buffer
+  first (O_DIRECT needs aligned source memory).
+* Data goes to ``*.tmp`` files that are renamed into place, and the manifest
+  is published last, so a build that fails or is interrupted never leaves a
+  store that opens.
+* INT8 K/V storage quantizes each page while it is written.
 """
 
 from __future__ import annotations
@@ -14,7 +23,7 @@ import errno
 import math
 import os
 import time
-from collections.abc import Iterable, Sequence
+from collections.abc import Iterable, Iterator, Sequence
 from pathlib import Path
 
 import torch
@@ -22,9 +31,63 @@ import torch
 from ..paged.layout import KVLayout, PageDescriptor, TensorLayout, build_page_descriptors
 from ..paged.memory import MemoryPageSource
 from ..quantization import quantize_int8_per_token_group
-from .direct_io import DIRECT_IO_ALIGNMENT, FORMAT_VERSION, AlignedFileWriter, atomic_write_json, fsync_directory
+from .direct_io import DIRECT_IO_ALIGNMENT, FORMAT_VERSION, PageBuffer, RecordFile, byte_view, publish_json, sync_directory
 from .qkv_store import NvmeQKVStore
 from .records import expected_file_size, kv_record_pages, q_record_pages
+
+
+class _RecordSink:
+    """Writes records given as (offset within the record, CPU tensor) pieces."""
+
+    def __init__(self, path: Path, largest_record: int, direct_io: bool) -> None:
+        self.file = RecordFile(path, write=True, direct_io=direct_io)
+        self.stage = PageBuffer(largest_record) if direct_io else None
+        self.zeros = None if direct_io else bytes(largest_record)
+
+    def write(self, page: PageDescriptor, pieces: Sequence[tuple[int, torch.Tensor]]) -> None:
+        size = page.storage_bytes
+        if self.stage is not None:
+            self.stage.bytes[:size].zero_()
+            for offset, tensor in pieces:
+                self.stage.put(offset, tensor)
+            window = self.stage.window(size)
+            try:
+                self.file.write_from(page.file_offset, window)
+            finally:
+                window.release()
+            return
+        views, cursor = [], 0
+        for offset, tensor in sorted(pieces, key=lambda piece: piece[0]):
+            if offset > cursor:
+                views.append(memoryview(self.zeros)[: offset - cursor])
+            data = byte_view(tensor.contiguous())
+            views.append(data)
+            cursor = offset + len(data)
+        if cursor < size:
+            views.append(memoryview(self.zeros)[: size - cursor])
+        self.file.write_from(page.file_offset, *views)
+
+    def finish(self) -> None:
+        self.file.close(sync=True)
+        self.release()
+
+    def release(self) -> None:
+        self.file.close()
+        if self.stage is not None:
+            self.stage.release()
+            self.stage = None
+
+
+def _take(pages: Iterator, what: str):
+    try:
+        return next(pages)
+    except StopIteration:
+        raise ValueError(f"{what} iterator ended early") from None
+
+
+def _expect_end(pages: Iterator, what: str) -> None:
+    if next(pages, None) is not None:
+        raise ValueError(f"{what} iterator yielded extra pages")
 
 
 class NvmeQKVWriter:
@@ -54,143 +117,122 @@ class NvmeQKVWriter:
         self.path.mkdir(parents=True, exist_ok=True)
         if (self.path / "manifest.json").exists():
             raise FileExistsError(f"store already exists: {self.path}")
-        self.q_tmp = self.path / "q.bin.tmp"
-        self.kv_tmp = self.path / "kv.bin.tmp"
-        self._temporary_paths = [self.q_tmp, self.kv_tmp, self.path / "manifest.json.tmp"]
+        paging = {"page_target_bytes": page_target_bytes, "token_alignment": block_n}
         self.q_pages = q_record_pages(
-            build_page_descriptors(self.cu_seqlens_q, bytes_per_token=q_layout.bytes_per_token,
-                                   page_target_bytes=page_target_bytes, token_alignment=block_n),
-            q_layout,
-        )
+            build_page_descriptors(self.cu_seqlens_q, bytes_per_token=q_layout.bytes_per_token, **paging), q_layout)
         self.kv_pages = kv_record_pages(
-            build_page_descriptors(self.cu_seqlens_k, bytes_per_token=kv_layout.storage_bytes_per_token,
-                                   page_target_bytes=page_target_bytes, token_alignment=block_n),
-            kv_layout,
-        )
+            build_page_descriptors(self.cu_seqlens_k, bytes_per_token=kv_layout.storage_bytes_per_token, **paging),
+            kv_layout)
+        self._staged = {"q": self.path / "q.bin.tmp", "kv": self.path / "kv.bin.tmp"}
+        self._published = {"q": self.path / "q.bin", "kv": self.path / "kv.bin"}
 
-    def _check_q(self, page: PageDescriptor, tensor: torch.Tensor) -> None:
-        expected = (page.valid_tokens, self.q_layout.heads, self.q_layout.head_dim)
-        if tensor.device.type != "cpu" or tuple(tensor.shape) != expected:
-            raise ValueError(f"query page {page.page_id} must use CPU shape {expected}")
-        if tensor.dtype != self.q_layout.torch_dtype:
+    # -- page checks (the reference's messages) -----------------------------
+    def _q_pieces(self, page: PageDescriptor, rows: torch.Tensor) -> list[tuple[int, torch.Tensor]]:
+        shape = (page.valid_tokens, self.q_layout.heads, self.q_layout.head_dim)
+        if rows.device.type != "cpu" or tuple(rows.shape) != shape:
+            raise ValueError(f"query page {page.page_id} must use CPU shape {shape}")
+        if rows.dtype != self.q_layout.torch_dtype:
             raise ValueError("query page dtype does not match q_layout")
+        return [(0, rows)]
 
-    def _check_kv(self, page: PageDescriptor, k: torch.Tensor, v: torch.Tensor) -> None:
-        expected = (page.valid_tokens, self.kv_layout.heads, self.kv_layout.head_dim)
+    def _kv_pieces(self, page: PageDescriptor, k: torch.Tensor, v: torch.Tensor,
+                   scratch: dict[str, torch.Tensor]) -> list[tuple[int, torch.Tensor]]:
+        layout = self.kv_layout
+        shape = (page.valid_tokens, layout.heads, layout.head_dim)
         if k.device.type != "cpu" or v.device.type != "cpu":
             raise ValueError("K/V writer pages must be CPU tensors")
-        if tuple(k.shape) != expected or tuple(v.shape) != expected:
-            raise ValueError(f"K/V page {page.page_id} must use shape {expected}")
-        if k.dtype != self.kv_layout.source_torch_dtype or v.dtype != k.dtype:
+        if tuple(k.shape) != shape or tuple(v.shape) != shape:
+            raise ValueError(f"K/V page {page.page_id} must use shape {shape}")
+        if k.dtype != layout.source_torch_dtype or v.dtype != k.dtype:
             raise ValueError("K/V page dtype does not match kv_layout")
+        if layout.storage_dtype != "int8":
+            return [(0, k), (page.v_offset, v)]
+        n = page.valid_tokens
+        groups = math.ceil(n / layout.quant_group_tokens)
+        started = time.perf_counter()
+        for name, source in (("k", k), ("v", v)):
+            quantize_int8_per_token_group(source, scratch[name][:n], scratch[name + "_scale"][:groups],
+                                          group_tokens=layout.quant_group_tokens)
+        self.quantization_seconds += time.perf_counter() - started
+        return [(0, scratch["k"][:n]), (page.v_offset, scratch["v"][:n]),
+                (page.k_scale_offset, scratch["k_scale"][:groups]), (page.v_scale_offset, scratch["v_scale"][:groups])]
 
-    @staticmethod
-    def _exhausted(iterator, what: str) -> None:
-        try:
-            next(iterator)
-        except StopIteration:
-            return
-        raise ValueError(f"{what} iterator yielded extra pages")
+    def _int8_scratch(self) -> dict[str, torch.Tensor]:
+        rows = max((p.padded_tokens for p in self.kv_pages), default=0)
+        if self.kv_layout.storage_dtype != "int8" or rows == 0:
+            return {}
+        shape = (rows, self.kv_layout.heads, self.kv_layout.head_dim)
+        groups = (math.ceil(rows / self.kv_layout.quant_group_tokens), self.kv_layout.heads)
+        return {"k": torch.empty(shape, dtype=torch.int8), "v": torch.empty(shape, dtype=torch.int8),
+                "k_scale": torch.empty(groups, dtype=torch.float16),
+                "v_scale": torch.empty(groups, dtype=torch.float16)}
+
+    def _manifest(self) -> dict[str, object]:
+        return {
+            "format": "seqattn-qkv",
+            "version": FORMAT_VERSION,
+            "alignment_bytes": DIRECT_IO_ALIGNMENT,
+            "page_target_bytes": self.page_target_bytes,
+            "block_n": self.block_n,
+            "q_layout": self.q_layout.as_dict(),
+            "kv_layout": self.kv_layout.as_dict(),
+            "cu_seqlens_q": list(self.cu_seqlens_q),
+            "cu_seqlens_k": list(self.cu_seqlens_k),
+            "q_pages": [p.as_dict() for p in self.q_pages],
+            "kv_pages": [p.as_dict() for p in self.kv_pages],
+            "files": {
+                "q": {"name": "q.bin", "size_bytes": expected_file_size(self.q_pages)},
+                "kv": {"name": "kv.bin", "size_bytes": expected_file_size(self.kv_pages)},
+            },
+            "quantization_seconds": self.quantization_seconds,
+        }
 
     def write_pages(
         self,
         q_pages: Iterable[torch.Tensor],
         kv_pages: Iterable[tuple[torch.Tensor, torch.Tensor]],
     ) -> NvmeQKVStore:
-        q_iter, kv_iter = iter(q_pages), iter(kv_pages)
-        q_file = kv_file = None
+        sinks: list[_RecordSink] = []
         try:
-            q_file = AlignedFileWriter(
-                self.q_tmp, max((p.storage_bytes for p in self.q_pages), default=DIRECT_IO_ALIGNMENT),
-                self.direct_io)
-            kv_file = AlignedFileWriter(
-                self.kv_tmp, max((p.storage_bytes for p in self.kv_pages), default=DIRECT_IO_ALIGNMENT),
-                self.direct_io)
+            largest = lambda pages: max((p.storage_bytes for p in pages), default=DIRECT_IO_ALIGNMENT)  # noqa: E731
+            q_sink = _RecordSink(self._staged["q"], largest(self.q_pages), self.direct_io)
+            sinks.append(q_sink)
+            kv_sink = _RecordSink(self._staged["kv"], largest(self.kv_pages), self.direct_io)
+            sinks.append(kv_sink)
+            q_iter = iter(q_pages)
             for page in self.q_pages:
-                tensor = next(q_iter, None)
-                if tensor is None:
-                    raise ValueError("query page iterator ended early")
-                self._check_q(page, tensor)
-                q_file.buffer.zero(page.storage_bytes)
-                q_file.buffer.copy_tensor(0, tensor)
-                q_file.write(page.file_offset, page.storage_bytes)
-            self._exhausted(q_iter, "query page")
-
-            int8 = self.kv_layout.storage_dtype == "int8"
-            most = max((p.padded_tokens for p in self.kv_pages), default=0)
-            if int8 and most:
-                shape = (most, self.kv_layout.heads, self.kv_layout.head_dim)
-                kq, vq = torch.empty(shape, dtype=torch.int8), torch.empty(shape, dtype=torch.int8)
-                groups_max = math.ceil(most / self.kv_layout.quant_group_tokens)
-                ks = torch.empty((groups_max, self.kv_layout.heads), dtype=torch.float16)
-                vs = torch.empty_like(ks)
+                q_sink.write(page, self._q_pieces(page, _take(q_iter, "query page")))
+            _expect_end(q_iter, "query page")
+            kv_iter = iter(kv_pages)
+            scratch = self._int8_scratch()
             for page in self.kv_pages:
-                pair = next(kv_iter, None)
-                if pair is None:
-                    raise ValueError("K/V page iterator ended early")
-                k, v = pair
-                self._check_kv(page, k, v)
-                kv_file.buffer.zero(page.storage_bytes)
-                if int8:
-                    n = page.valid_tokens
-                    groups = math.ceil(n / self.kv_layout.quant_group_tokens)
-                    started = time.perf_counter()
-                    quantize_int8_per_token_group(k, kq[:n], ks[:groups],
-                                                  group_tokens=self.kv_layout.quant_group_tokens)
-                    quantize_int8_per_token_group(v, vq[:n], vs[:groups],
-                                                  group_tokens=self.kv_layout.quant_group_tokens)
-                    self.quantization_seconds += time.perf_counter() - started
-                    kv_file.buffer.copy_tensor(0, kq[:n])
-                    kv_file.buffer.copy_tensor(page.v_offset, vq[:n])
-                    kv_file.buffer.copy_tensor(page.k_scale_offset, ks[:groups])
-                    kv_file.buffer.copy_tensor(page.v_scale_offset, vs[:groups])
-                else:
-                    kv_file.buffer.copy_tensor(0, k)
-                    kv_file.buffer.copy_tensor(page.v_offset, v)
-                kv_file.write(page.file_offset, page.storage_bytes)
-            self._exhausted(kv_iter, "K/V page")
-
-            q_file.close()
-            kv_file.close()
-            q_file = kv_file = None
-            if self.q_tmp.stat().st_size != expected_file_size(self.q_pages):
-                raise OSError(errno.EIO, "query file size does not match its page table")
-            if self.kv_tmp.stat().st_size != expected_file_size(self.kv_pages):
-                raise OSError(errno.EIO, "K/V file size does not match its page table")
-            os.replace(self.q_tmp, self.path / "q.bin")
-            os.replace(self.kv_tmp, self.path / "kv.bin")
-            fsync_directory(self.path)
-            atomic_write_json(self.path / "manifest.json", {
-                "format": "seqattn-qkv",
-                "version": FORMAT_VERSION,
-                "alignment_bytes": DIRECT_IO_ALIGNMENT,
-                "page_target_bytes": self.page_target_bytes,
-                "block_n": self.block_n,
-                "q_layout": self.q_layout.as_dict(),
-                "kv_layout": self.kv_layout.as_dict(),
-                "cu_seqlens_q": list(self.cu_seqlens_q),
-                "cu_seqlens_k": list(self.cu_seqlens_k),
-                "q_pages": [p.as_dict() for p in self.q_pages],
-                "kv_pages": [p.as_dict() for p in self.kv_pages],
-                "files": {
-                    "q": {"name": "q.bin", "size_bytes": expected_file_size(self.q_pages)},
-                    "kv": {"name": "kv.bin", "size_bytes": expected_file_size(self.kv_pages)},
-                },
-                "quantization_seconds": self.quantization_seconds,
-            })
-            return NvmeQKVStore(self.path, direct_io=self.direct_io)
+                k, v = _take(kv_iter, "K/V page")
+                kv_sink.write(page, self._kv_pieces(page, k, v, scratch))
+            _expect_end(kv_iter, "K/V page")
+            for sink in sinks:
+                sink.finish()
+            sinks = []
+            for key, pages, what in (("q", self.q_pages, "query"), ("kv", self.kv_pages, "K/V")):
+                if self._staged[key].stat().st_size != expected_file_size(pages):
+                    raise OSError(errno.EIO, f"{what} file size does not match its page table")
+            for key in ("q", "kv"):
+                os.replace(self._staged[key], self._published[key])
+            sync_directory(self.path)
+            publish_json(self.path / "manifest.json", self._manifest())
         except BaseException:
-            for f in (q_file, kv_file):
-                if f is not None:
-                    f.close()
+            for sink in sinks:
+                sink.release()
             self.abort()
             raise
+        return NvmeQKVStore(self.path, direct_io=self.direct_io)
 
     def abort(self) -> None:
-        paths = list(self._temporary_paths)
+        """Remove everything an unfinished build wrote (a published store,
+        one with a manifest, is left alone)."""
+        leftovers = [*self._staged.values(), self.path / "manifest.json.tmp"]
         if not (self.path / "manifest.json").exists():
-            paths += [self.path / "q.bin", self.path / "kv.bin"]
-        for path in paths:
+            leftovers += list(self._published.values())
+        for path in leftovers:
             path.unlink(missing_ok=True)
 
     @classmethod
@@ -209,14 +251,15 @@ class NvmeQKVWriter:
         quant_group_tokens: int = 64,
         direct_io: bool = True,
     ) -> NvmeQKVStore:
-        layout_source = MemoryPageSource(
+        # The in-memory source validates the tensors and derives the layouts.
+        source = MemoryPageSource(
             q=q, k=k, v=v, cu_seqlens_q=cu_seqlens_q, cu_seqlens_k=cu_seqlens_k,
             page_target_bytes=page_target_bytes, block_n=block_n,
             kv_storage_dtype=kv_storage_dtype, quant_group_tokens=quant_group_tokens,
         )
         writer = cls(
-            path, q_layout=layout_source.q_layout, kv_layout=layout_source.kv_layout,
-            cu_seqlens_q=layout_source.cu_seqlens_q or (), cu_seqlens_k=layout_source.cu_seqlens_k or (),
+            path, q_layout=source.q_layout, kv_layout=source.kv_layout,
+            cu_seqlens_q=source.cu_seqlens_q or (), cu_seqlens_k=source.cu_seqlens_k or (),
             page_target_bytes=page_target_bytes, block_n=block_n, direct_io=direct_io,
         )
         return writer.write_pages(

@@ -44,6 +44,8 @@ class StreamingAttentionRunner(HipExecutorMixin):
             raise ValueError("attention plan output_mode does not match runner config")
         self.backend = resolve_backend(self.config.backend, plan.dtype, plan.device, head_dim=plan.head_dim)
         self._workspace = CudaWorkspace(plan)
+        if self.config.enable_nvtx:
+            self._workspace.enable_trace_ranges()
 
     def close(self) -> None:
         """Release the pipeline's streams and events (buffers follow the runner)."""

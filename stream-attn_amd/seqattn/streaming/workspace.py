@@ -114,6 +114,12 @@ class CudaWorkspace:
         self.resident_scratch: torch.Tensor | None = None
         _LIVE.add(self)
 
+    def enable_trace_ranges(self) -> None:
+        """Bracket each pipeline stage's enqueue with ROCm tracer ranges named
+        like the reference's NVTX ranges (seqattn:q_h2d, kv_h2d, fused_update,
+        fused_finalize, output_d2h)."""
+        _native.check(self._lib.sa_pipeline_set_trace_ranges(self.handle, 1), "sa_pipeline_set_trace_ranges")
+
     def _attach(self, buffer: torch.Tensor | None) -> None:
         status = self._lib.sa_pipeline_attach_resident_scratch(
             self.handle, None if buffer is None else buffer.data_ptr(), 0 if buffer is None else buffer.numel()

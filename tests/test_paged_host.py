@@ -369,7 +369,9 @@ def test_store_round_trip_buffered(tmp_path):
             assert torch.equal(k_rec[: page.valid_tokens], k[page.token_start : page.token_stop])
             assert torch.equal(v_rec[: page.valid_tokens], v[page.token_start : page.token_stop])
             assert torch.all(k_rec[page.valid_tokens :] == 0)
-        assert plan.snapshot().direct_io_bounce_peak_bytes > 0
+        # Buffered stores read rows straight into the caller's tensors: no
+        # bounce memory is charged.
+        assert plan.snapshot().direct_io_bounce_peak_bytes == 0
     finally:
         reader.close()
     assert plan.snapshot().direct_io_bounce_allocated_bytes == 0
@@ -447,13 +449,23 @@ def test_direct_io_round_trip_when_supported(tmp_path):
                                            block_n=16, kv_storage_dtype="bf16", direct_io=True)
     except RuntimeError as error:
         pytest.skip(f"test filesystem has no O_DIRECT support: {error}")
-    reader = store.open_reader(small_plan(), 1)
+    plan = small_plan()
+    reader = store.open_reader(plan, 1)
     page = store.q_pages[0]
     out = torch.empty((page.padded_tokens, 4, 16), dtype=q.dtype)
     try:
         reader.read_q(page, out)
+        # O_DIRECT reads go through aligned page buffers charged as bounce memory.
+        assert plan.snapshot().direct_io_bounce_allocated_bytes > 0
+        for kv_page in store.kv_pages:
+            ko = torch.empty((kv_page.padded_tokens, 2, 16), dtype=k.dtype)
+            vo = torch.empty_like(ko)
+            reader.read_kv(kv_page, ko, vo)
+            assert torch.equal(ko[: kv_page.valid_tokens], k[kv_page.token_start : kv_page.token_stop])
+            assert torch.equal(vo[: kv_page.valid_tokens], v[kv_page.token_start : kv_page.token_stop])
     finally:
         reader.close()
+    assert plan.snapshot().direct_io_bounce_allocated_bytes == 0
     assert torch.equal(out[: page.valid_tokens], q[: page.valid_tokens])
 
 

@@ -139,3 +139,34 @@ def test_planned_workspace_is_monotone_in_budget():
         assert plan.q_chunk_tokens == 524288 or bigger > gib * 2**30
         previous = plan.q_chunk_tokens
     assert math.ceil(524288 / previous) == 3
+
+
+def test_measured_rates_pick_fewest_passes_on_a_slow_link_and_large_chunks_when_kernel_bound():
+    from seqattn.planner import PlannerRates, modeled_run
+
+    shape = dict(q_heads=56, kv_heads=56, head_dim=128, dtype=torch.bfloat16, device="cpu",
+                 max_q_tokens=524_288, max_kv_tokens=524_288)
+    config = StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30)
+    slow = build_plan(**shape, config=config, rates=PlannerRates(h2d_bytes_per_second=1e9,
+                                                                 update_flops_per_second=1.1e15))
+    fast = build_plan(**shape, config=config, rates=PlannerRates(h2d_bytes_per_second=1e15,
+                                                                 update_flops_per_second=1.1e15))
+    # A slow link makes re-streaming K/V dominate: the smallest ring and so the
+    # largest Q block (fewest passes) wins.  A kernel-bound run saves FP32
+    # state traffic and launches with the largest chunk.
+    assert slow.kv_chunk_tokens == 4096 and slow.h2d_link_fraction > 0.99
+    assert fast.kv_chunk_tokens == 16384 and fast.h2d_link_fraction < 0.01
+    for plan in (slow, fast):
+        assert plan.estimated_workspace_bytes <= 2 * 2**30
+        seconds, fraction = modeled_run(q_chunk=plan.q_chunk_tokens, kv_chunk=plan.kv_chunk_tokens,
+                                        max_q_tokens=524_288, max_kv_tokens=524_288, q_heads=56, kv_heads=56,
+                                        head_dim=128, dtype=torch.bfloat16,
+                                        rates=PlannerRates(h2d_bytes_per_second=1e9, update_flops_per_second=1.1e15)
+                                        if plan is slow else
+                                        PlannerRates(h2d_bytes_per_second=1e15, update_flops_per_second=1.1e15))
+        assert seconds == plan.estimated_seconds and 0 < fraction <= 1
+    # The modeled kernel time of a kernel-bound run is at least its FLOP at the rate.
+    assert fast.estimated_seconds >= 4 * 56 * 128 * 524_288**2 / 1.1e15
+    # Without rates the reference's choice stands (README.md:62).
+    plain = build_plan(**shape, config=config)
+    assert (plain.q_chunk_tokens, plain.kv_chunk_tokens, plain.estimated_seconds) == (28_416, 8_192, None)
