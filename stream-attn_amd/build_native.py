@@ -19,13 +19,9 @@ CSRC = PACKAGE_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 LIB_DIR = PACKAGE_ROOT / "seqattn" / "_lib"
 LIB_PATH = LIB_DIR / "libseqattn_hip.so"
-DRIVER_PATH = LIB_DIR / "sa_pipeline_driver"
 ARCH = "gfx950"
 
 SOURCES = ("sa_kernels.hip", "sa_pipeline.cpp")
-# Native driver of the pinned-DRAM path over the C-ABI (no Python in the
-# process), used to trace copy-engine activity; linked against the library.
-DRIVER_SOURCE = "sa_pipeline_driver.cpp"
 
 # Device-side flags.  Packed FP32 VALU instructions are disabled for all
 # device code.
@@ -80,32 +76,7 @@ def build(verbose: bool = False) -> Path:
     if verbose and stderr.strip():
         print(stderr, file=sys.stderr)
     os.replace(tmp, LIB_PATH)
-    build_driver(verbose)
     return LIB_PATH
-
-
-def build_driver(verbose: bool = False) -> Path:
-    """Compile the native pipeline driver next to the library (rpath $ORIGIN)."""
-    tmp = DRIVER_PATH.with_suffix(".tmp")
-    cmd = [
-        hipcc(),
-        "-O2",
-        "-std=c++17",
-        f"-I{INCLUDE}",
-        str(CSRC / DRIVER_SOURCE),
-        f"-L{LIB_DIR}",
-        "-lseqattn_hip",
-        "-Wl,-rpath,$ORIGIN",
-        "-o",
-        str(tmp),
-    ]
-    if verbose:
-        print(" ".join(cmd), flush=True)
-    result = subprocess.run(cmd, capture_output=True, text=True)
-    if result.returncode != 0:
-        raise RuntimeError(f"hipcc failed for {DRIVER_SOURCE} ({result.returncode}):\n{result.stderr}")
-    os.replace(tmp, DRIVER_PATH)
-    return DRIVER_PATH
 
 
 if __name__ == "__main__":

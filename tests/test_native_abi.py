@@ -92,17 +92,3 @@ def test_int8_update_argument_errors_surface_without_a_gpu():
     assert call(64, group=48) == -1 and b"power of two" in lib.sa_last_error()
     assert call(64, offset=-1) == -1
     assert call(64) == -1 and b"null pointer" in lib.sa_last_error()
-
-
-DRIVER = Path(__file__).resolve().parents[1] / "stream-attn_amd" / "seqattn" / "_lib" / "sa_pipeline_driver"
-
-
-@pytest.mark.skipif(not DRIVER.exists(), reason="native pipeline driver not built")
-@pytest.mark.parametrize("args", [[], ["524288", "56", "128", "28416", "8192", "4", "1"],
-                                  ["1024", "8", "64", "512", "256", "2", "0"]])
-def test_pipeline_driver_rejects_bad_arguments_before_touching_the_gpu(args):
-    import subprocess
-
-    result = subprocess.run([str(DRIVER), *args], capture_output=True, text=True, timeout=60)
-    assert result.returncode == 2
-    assert ("usage" in result.stderr) if not args else ("invalid arguments" in result.stderr)
