@@ -404,6 +404,32 @@ int32_t sa_pipeline_kernel_timing(sa_pipeline* pipeline, double* total_ms, int64
 int32_t sa_pipeline_kernel_busy(sa_pipeline* pipeline, double* busy_ms, double* total_ms,
                                 int64_t* launches);
 
+/*
+ * sa_run_resident_noalloc: attention over HBM-resident Q/K/V into a
+ * caller-owned device output (and LSE), allocating nothing.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  It computes what sa_pipeline_run_resident computes for
+ * head_dim 128 with transposed-V scratch attached, bit for bit (same
+ * launches: a V transpose per segment, then one fused update launch whose
+ * row sums merge at every kv_chunk_tokens boundary), but the transposed V
+ * lives in a fixed 64 MiB device array inside the library (one per GPU,
+ * held until the process ends) instead of caller-provided scratch.
+ * Limits: head_dim 128; per segment kv_heads * 128 * (keys rounded up to
+ * 64) * 2 bytes <= 64 MiB (for example 8 K/V heads x 32,768 keys), larger
+ * segments are rejected before anything is enqueued.  Calls on one GPU share
+ * its array: calls that overlap on that GPU (other streams or threads) race.
+ * Strides are in elements; lse may be NULL.  Enqueued on `stream`.
+ */
+int32_t sa_run_resident_noalloc(const void* q, const void* k, const void* v, void* out, float* lse,
+                                int64_t stride_qt, int64_t stride_qh, int64_t stride_kt,
+                                int64_t stride_kh, int64_t stride_vt, int64_t stride_vh,
+                                int64_t stride_ot, int64_t stride_oh, int64_t lse_stride_h,
+                                const int64_t* cu_seqlens_q, const int64_t* cu_seqlens_k,
+                                int32_t num_segments, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, int32_t dtype, int32_t kv_chunk_tokens,
+                                double softmax_scale, int32_t causal, void* stream);
+
 /* hipStream_t of the pipeline's H2D (which == 0) or D2H (which == 1) copy stream. */
 void* sa_pipeline_stream(sa_pipeline* pipeline, int32_t which);
 

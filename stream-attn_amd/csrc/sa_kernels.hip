@@ -64,6 +64,7 @@
 
 #include <cmath>
 #include <cstdint>
+#include <mutex>
 
 #include "sa_common.h"
 
@@ -888,7 +889,9 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
     return SA_ERR_INVALID_ARGUMENT;
   }
   if (q_tokens == 0) return 0;
-  if (!q || !k || !v || !m || !l || !acc) {
+  // A fused launch initializes its state and writes the output instead of
+  // the state: m, l and acc are not touched and may be null.
+  if (!q || !k || !v || (fused == nullptr && (!m || !l || !acc))) {
     set_error("sa_update_attention_state: null pointer argument");
     return SA_ERR_INVALID_ARGUMENT;
   }
@@ -1129,7 +1132,129 @@ int32_t launch_finalize(const float* acc, const float* m, const float* l, void* 
 
 }  // namespace sa
 
+namespace {
+
+// Device scratch of sa_run_resident_noalloc: the transposed copy of V that
+// the resident update launch reads.  One array per GPU, held from the first
+// load of this library's code object until the process ends.  In host code
+// the name is only a stand-in for the symbol: the array's address on a
+// device comes from hipGetSymbolAddress with that device current, looked up
+// once per device and kept below.
+constexpr int64_t kNoAllocScratchBytes = int64_t(64) << 20;
+constexpr int kMaxDevices = 64;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::mutex g_scratch_mutex;
+void* g_scratch_address[kMaxDevices] = {};
+
+int32_t scratch_on_current_device(void** address) {
+  int device = 0;
+  hipError_t err = hipGetDevice(&device);
+  if (err != hipSuccess) return sa::hip_status(err, "sa_run_resident_noalloc: hipGetDevice");
+  if (device < 0 || device >= kMaxDevices) {
+    sa::set_error("sa_run_resident_noalloc: device ordinal %d outside [0, %d)", device, kMaxDevices);
+    return SA_ERR_BAD_STATE;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_address[device] == nullptr) {
+    void* found = nullptr;
+    err = hipGetSymbolAddress(&found, HIP_SYMBOL(scratch));
+    if (err != hipSuccess) return sa::hip_status(err, "sa_run_resident_noalloc: hipGetSymbolAddress(scratch)");
+    if (found == nullptr || reinterpret_cast<uintptr_t>(found) % 256 != 0) {
+      sa::set_error("sa_run_resident_noalloc: scratch address %p is not 256-byte aligned", found);
+      return SA_ERR_BAD_STATE;
+    }
+    g_scratch_address[device] = found;
+  }
+  *address = g_scratch_address[device];
+  return 0;
+}
+
+}  // namespace
+
 extern "C" {
+
+int32_t sa_run_resident_noalloc(const void* q, const void* k, const void* v, void* out, float* lse,
+                                int64_t stride_qt, int64_t stride_qh, int64_t stride_kt,
+                                int64_t stride_kh, int64_t stride_vt, int64_t stride_vh,
+                                int64_t stride_ot, int64_t stride_oh, int64_t lse_stride_h,
+                                const int64_t* cu_seqlens_q, const int64_t* cu_seqlens_k,
+                                int32_t num_segments, int32_t q_heads, int32_t kv_heads,
+                                int32_t head_dim, int32_t dtype, int32_t kv_chunk_tokens,
+                                double softmax_scale, int32_t causal, void* stream) {
+  sa::clear_error();
+  if (!q || !k || !v || !out || !cu_seqlens_q || !cu_seqlens_k || num_segments < 0) {
+    sa::set_error("sa_run_resident_noalloc: null argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (head_dim != 128) {
+    sa::set_error("sa_run_resident_noalloc: the transposed-V launch needs head_dim 128, got %d", head_dim);
+    return SA_ERR_UNSUPPORTED_HEAD_DIM;
+  }
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
+    sa::set_error("sa_run_resident_noalloc: unsupported dtype code %d", dtype);
+    return SA_ERR_UNSUPPORTED_DTYPE;
+  }
+  if (q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || kv_chunk_tokens <= 0 ||
+      kv_chunk_tokens % 64 != 0) {
+    sa::set_error("sa_run_resident_noalloc: bad heads %d/%d or K/V chunk %d (a positive multiple of 64)",
+                  q_heads, kv_heads, kv_chunk_tokens);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (stride_ot % 8 != 0 || stride_oh % 8 != 0 || !aligned(out, 16)) {
+    sa::set_error("sa_run_resident_noalloc: out must be 16-byte aligned with strides that are multiples of 8");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  // Every segment is checked before anything is enqueued.
+  for (int32_t s = 0; s < num_segments; ++s) {
+    const int64_t q_length = cu_seqlens_q[s + 1] - cu_seqlens_q[s];
+    const int64_t k_length = cu_seqlens_k[s + 1] - cu_seqlens_k[s];
+    if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0) || q_length > INT32_MAX ||
+        k_length >= (1 << 24)) {
+      sa::set_error("sa_run_resident_noalloc: segment %d has invalid bounds", s);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    const int64_t needed = (int64_t)kv_heads * 128 * ((k_length + 63) / 64 * 64) * 2;
+    if (q_length > 0 && needed > kNoAllocScratchBytes) {
+      sa::set_error("sa_run_resident_noalloc: segment %d needs %lld bytes of transposed-V scratch; this entry "
+                    "point has %lld (kv_heads * 128 * keys rounded up to 64 * 2 bytes per segment)",
+                    s, (long long)needed, (long long)kNoAllocScratchBytes);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+  }
+  void* vt = nullptr;
+  int32_t rc = scratch_on_current_device(&vt);
+  if (rc != 0) return rc;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  const char* qd = static_cast<const char*>(q);
+  const char* kd = static_cast<const char*>(k);
+  const char* vd = static_cast<const char*>(v);
+  char* od = static_cast<char*>(out);
+  for (int32_t s = 0; s < num_segments; ++s) {
+    const int64_t q_start = cu_seqlens_q[s], k_start = cu_seqlens_k[s];
+    const int64_t q_length = cu_seqlens_q[s + 1] - q_start, k_length = cu_seqlens_k[s + 1] - k_start;
+    if (q_length == 0) continue;
+    // The launch sequence of sa_pipeline_run_resident's fused path with the
+    // scratch in place of the attached one: V transposed (zero keys up to
+    // the 64-key tile), then one update launch over the segment that
+    // finalizes in its epilogue with the row sums merged at every K/V chunk
+    // boundary.  Both launches are on `stream`, so a later segment's
+    // transpose starts after this segment's update has read the scratch.
+    const int64_t t_pad = (k_length + 63) / 64 * 64;
+    const char* v_seg = vd + k_start * stride_vt * 2;
+    rc = sa::launch_transpose_v(v_seg, stride_vt, stride_vh, (int32_t)k_length, kv_heads, 128, vt, t_pad, hs);
+    if (rc != 0) return rc;
+    const sa::FusedOutput fused{od + q_start * stride_ot * 2, stride_ot, stride_oh, lse, lse_stride_h, q_start};
+    rc = sa::launch_update(qd + q_start * stride_qt * 2, kd + k_start * stride_kt * 2, vt, nullptr, nullptr,
+                           nullptr, stride_qt, stride_qh, stride_kt, stride_kh, t_pad, 128 * t_pad, 0, 0, 0, 0,
+                           (int32_t)q_length, (int32_t)k_length, q_heads, kv_heads, 128, 0, 0,
+                           (int32_t)(k_length - q_length), softmax_scale,
+                           (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, dtype, hs, kv_chunk_tokens, &fused,
+                           true);
+    if (rc != 0) return rc;
+  }
+  return 0;
+}
 
 int32_t sa_update_attention_state(const void* q, const void* k, const void* v, float* running_max,
                                   float* running_sum, float* accumulator, int64_t stride_qt,

@@ -110,6 +110,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         + [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64), c_int32, c_double, c_int32, c_void_p,
            ctypes.POINTER(PipelineStats)],
     ),
+    "sa_run_resident_noalloc": (
+        c_int32,
+        [c_void_p] * 4 + [c_void_p] + [c_int64] * 9
+        + [ctypes.POINTER(c_int64), ctypes.POINTER(c_int64)] + [c_int32] * 6 + [c_double, c_int32, c_void_p],
+    ),
     "sa_pipeline_finalize": (
         c_int32, [c_void_p, c_int32, c_int32, c_void_p, c_int64, c_int64, c_void_p]
     ),

@@ -92,3 +92,27 @@ def test_int8_update_argument_errors_surface_without_a_gpu():
     assert call(64, group=48) == -1 and b"power of two" in lib.sa_last_error()
     assert call(64, offset=-1) == -1
     assert call(64) == -1 and b"null pointer" in lib.sa_last_error()
+
+
+@pytest.mark.skipif(not _native.library_is_built(), reason="native library not built")
+def test_noalloc_entry_point_rejects_bad_arguments_before_touching_the_gpu():
+    import ctypes
+
+    lib = _native.lib()
+    fake = 1 << 40  # never dereferenced: every case below is rejected by the host-side checks
+
+    def call(cu_q, cu_k, *, heads=(8, 2), head_dim=128, dtype=0, kv_chunk=8192, q=fake):
+        qa = (ctypes.c_int64 * len(cu_q))(*cu_q)
+        ka = (ctypes.c_int64 * len(cu_k))(*cu_k)
+        return lib.sa_run_resident_noalloc(q, fake, fake, fake, None, *([8 * 128] * 9), qa, ka, len(cu_q) - 1,
+                                           heads[0], heads[1], head_dim, dtype, kv_chunk, 0.1, 0, None)
+
+    assert call([0, 10], [0, 10], head_dim=64) == -3 and b"head_dim 128" in lib.sa_last_error()
+    assert call([0, 10], [0, 10], dtype=7) == -2
+    assert call([0, 10], [0, 10], kv_chunk=100) == -1 and b"multiple of 64" in lib.sa_last_error()
+    assert call([0, 10], [0, 10], q=None) == -1 and b"null" in lib.sa_last_error()
+    assert call([0, 10], [0, 0]) == -1 and b"invalid bounds" in lib.sa_last_error()
+    # 2 K/V heads x 128 x 131,072 keys x 2 bytes = 64 MiB fits; one more tile does not.
+    assert call([0, 1, 2], [0, 131_072, 131_072 + 131_073]) == -1
+    message = lib.sa_last_error()
+    assert b"segment 1 needs" in message and b"67108864" in message
