@@ -161,8 +161,14 @@ typedef struct sa_pipeline_stats {
  *
  *   q_buffer      [q_chunk_tokens, q_heads, head_dim] dtype
  *   k_slots[i], v_slots[i]  [kv_chunk_tokens, kv_heads, head_dim] dtype, i < num_kv_buffers (1..3)
- *   running_max, running_sum [q_chunk_tokens, q_heads] fp32
- *   accumulator   [q_chunk_tokens, q_heads, head_dim] fp32
+ *   running_max, running_sum  q_rows * q_heads fp32
+ *   accumulator   q_rows * q_heads * head_dim fp32
+ *                 with q_rows = q_chunk_tokens rounded up to a multiple of 32.
+ *                 The pipeline keeps this state in the update kernel's
+ *                 row-group layout (32-row groups in lane order, so every
+ *                 state load and store moves whole contiguous blocks), not in
+ *                 the strided [token][head] layout of sa_update_attention_state;
+ *                 only this pipeline's launches read it.
  *   out_slots     NULL (device-consumer mode: no raw output buffers) or
  *                 num_output_buffers pointers to [q_chunk_tokens, q_heads, head_dim] dtype
  *   num_output_buffers  1..2: output ready/free event pairs (and slots when out_slots != NULL)

@@ -73,7 +73,8 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
                       hipStream_t stream, int32_t merge_keys = 0,
-                      const FusedOutput* fused = nullptr, bool v_transposed = false);
+                      const FusedOutput* fused = nullptr, bool v_transposed = false,
+                      bool tiled_state = false);
 // V [kv_tokens, kv_heads, 128] -> vt [kv_heads][128][t_pad] in the key order
 // the update kernel's transposed-V variant reads, zero keys up to t_pad.
 int32_t launch_transpose_v(const void* v, int64_t sv_t, int64_t sv_h, int32_t kv_tokens, int32_t kv_heads,
@@ -87,9 +88,12 @@ int32_t launch_update_int8(const void* q, const void* k, const void* v, const vo
                            int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                            int32_t storage_token_offset, int32_t causal_shift,
                            double softmax_scale, int32_t flags, int32_t dtype,
-                           int32_t quant_group_tokens, hipStream_t stream);
+                           int32_t quant_group_tokens, hipStream_t stream, bool tiled_state = false);
 int32_t launch_finalize(const float* acc, const float* m, const float* l, void* out, float* lse,
                         int64_t sa_t, int64_t sa_h, int64_t ss_t, int64_t ss_h, int64_t so_t,
                         int64_t so_h, int64_t lse_sh, int64_t lse_off, int32_t q_tokens,
-                        int32_t q_heads, int32_t head_dim, int32_t dtype, hipStream_t stream);
+                        int32_t q_heads, int32_t head_dim, int32_t dtype, hipStream_t stream,
+                        bool tiled_state = false);
+// tiled_state: m, l and acc are the pipeline's own buffers in the row-group
+// layout (32-row groups, lane order; see the update kernel), not strided.
 }  // namespace sa

@@ -143,7 +143,23 @@ struct UpdateParams {
   int64_t so_t = 0, so_h = 0;
   float* lse = nullptr;
   int64_t lse_sh = 0, lse_off = 0;
+  // State in the pipeline's row-group layout (state_offset) instead of the
+  // strided [token][head] layout given by ss_* / sa_*.
+  int32_t tiled_state = 0;
 };
+
+// Pipeline-owned FP32 state is kept in the order the update kernel's lanes
+// hold it.  Rows form groups of 32 (a wave's query block); group g of head h
+// is one block of 32 * head_dim floats (and 32 floats of m, of l) at block
+// index g * q_heads + h, so row r of a buffer sits where the token-major
+// layout would put it, rounded to its 32-row group.  Within a block, 4-float
+// chunk c (d = 4c .. 4c + 3) of row lr is at (c * 32 + lr) * 4: the 64 lanes
+// of a wave, (lr, hf) holding chunk 2 * (8 db + 2 g) / 2 + hf, read or write
+// 1 KB contiguously per instruction, where the strided layout touched 32
+// rows 28 KB apart with 32 bytes each.
+__device__ inline int64_t state_block(int64_t row, int head, int q_heads) {
+  return (row >> 5) * q_heads + head;
+}
 
 // Row r (0..15) of a 32x32 C tile held in register i of a lane in half h.
 __device__ inline int c_row(int i, int h) { return 8 * (i >> 2) + 4 * h + (i & 3); }
@@ -280,17 +296,19 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
 #pragma unroll
     for (int d = 0; d < DB; ++d) acc[qb][d] = f32x16{};
     if (!INIT && qi[qb] < p.q_tokens) {
-      const int64_t srow = (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+      const int64_t blk = state_block(qi[qb], head, p.q_heads);
+      const int64_t srow = p.tiled_state ? blk * 32 + lr : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
       m_run[qb] = p.m[srow];
       l_part[qb] = hf == 0 ? p.l[srow] : 0.f;
-      const float* arow = p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
+      const float* arow = p.tiled_state ? p.acc + blk * 32 * p.head_dim + 4 * lr
+                                        : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
           const int col = 32 * d + 8 * g + 4 * hf;
           if (col < p.head_dim) {
-            const f32x4 v4 = *reinterpret_cast<const f32x4*>(arow + col);
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(arow + (p.tiled_state ? 32 * col : col));
             acc[qb][d][4 * g + 0] = v4[0];
             acc[qb][d][4 * g + 1] = v4[1];
             acc[qb][d][4 * g + 2] = v4[2];
@@ -699,12 +717,14 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
             l_full > 0.f ? (m_run[qb] + log2f(l_full)) * 0.69314718055994530942f : -INFINITY;
       continue;
     }
-    const int64_t srow = (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+    const int64_t blk = state_block(qi[qb], head, p.q_heads);
+    const int64_t srow = p.tiled_state ? blk * 32 + lr : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
     if (hf == 0) {
       p.m[srow] = m_run[qb];
       p.l[srow] = l_full;
     }
-    float* arow = p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
+    float* arow = p.tiled_state ? p.acc + blk * 32 * p.head_dim + 4 * lr
+                                : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
 #pragma unroll
@@ -713,7 +733,7 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
         if (col < p.head_dim) {
           const f32x4 v4 = {acc[qb][d][4 * g + 0], acc[qb][d][4 * g + 1], acc[qb][d][4 * g + 2],
                             acc[qb][d][4 * g + 3]};
-          *reinterpret_cast<f32x4*>(arow + col) = v4;
+          *reinterpret_cast<f32x4*>(arow + (p.tiled_state ? 32 * col : col)) = v4;
         }
       }
     }
@@ -729,6 +749,7 @@ struct FinalizeParams {
   int64_t sa_t, sa_h, ss_t, ss_h, so_t, so_h, lse_sh, lse_off;
   int64_t total;  // q_tokens * q_heads * (head_dim / 8)
   int32_t q_heads, groups;
+  int32_t tiled_state;  // state in the row-group layout (state_block)
 };
 
 template <typename Op>
@@ -739,10 +760,21 @@ __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
   const int64_t row = idx / p.groups;
   const int h = (int)(row % p.q_heads);
   const int64_t t = row / p.q_heads;
-  const float l = p.l[t * p.ss_t + h * p.ss_h];
-  const float* a = p.acc + t * p.sa_t + h * p.sa_h + 8 * g;
-  const f32x4 a0 = *reinterpret_cast<const f32x4*>(a);
-  const f32x4 a1 = *reinterpret_cast<const f32x4*>(a + 4);
+  const int64_t blk = state_block(t, h, p.q_heads);
+  const int lr = (int)(t & 31);
+  const int64_t srow = p.tiled_state ? blk * 32 + lr : t * p.ss_t + h * p.ss_h;
+  const float l = p.l[srow];
+  f32x4 a0, a1;
+  if (p.tiled_state) {
+    // Chunks 2g and 2g + 1 (d = 8g .. 8g + 7) of row lr.
+    const float* a = p.acc + blk * 32 * (p.groups * 8) + (2 * g * 32 + lr) * 4;
+    a0 = *reinterpret_cast<const f32x4*>(a);
+    a1 = *reinterpret_cast<const f32x4*>(a + 32 * 4);
+  } else {
+    const float* a = p.acc + t * p.sa_t + h * p.sa_h + 8 * g;
+    a0 = *reinterpret_cast<const f32x4*>(a);
+    a1 = *reinterpret_cast<const f32x4*>(a + 4);
+  }
   u32x4 o;
   if (l > 0.f) {
     o[0] = Op::pack2(a0[0] / l, a0[1] / l);
@@ -754,7 +786,7 @@ __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
   }
   *reinterpret_cast<u32x4*>(p.out + t * p.so_t + h * p.so_h + 8 * g) = o;
   if (p.lse != nullptr && g == 0) {
-    const float m = p.m[t * p.ss_t + h * p.ss_h];
+    const float m = p.m[srow];
     p.lse[h * p.lse_sh + p.lse_off + t] =
         l > 0.f ? (m + log2f(l)) * 0.69314718055994530942f : -INFINITY;
   }
@@ -873,7 +905,7 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                       int32_t causal_shift, double softmax_scale, int32_t flags, int32_t dtype,
                       hipStream_t stream, int32_t merge_keys, const FusedOutput* fused,
-                      bool v_transposed) {
+                      bool v_transposed, bool tiled_state) {
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
     set_error("sa_update_attention_state: unsupported dtype code %d", dtype);
     return SA_ERR_UNSUPPORTED_DTYPE;
@@ -935,6 +967,7 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
     return SA_ERR_INVALID_ARGUMENT;
   }
   p.merge_tiles = merge_keys / 64;
+  p.tiled_state = tiled_state ? 1 : 0;
   if (fused != nullptr) {
     // Same output layout rules as the finalize kernel.
     if (!(flags & SA_FLAG_INITIALIZE) || !fused->out || fused->so_t % 8 != 0 || fused->so_h % 8 != 0 ||
@@ -984,7 +1017,7 @@ int32_t launch_update_int8(const void* q, const void* k, const void* v, const vo
                            int32_t head_dim, int32_t q_local_offset, int32_t kv_local_offset,
                            int32_t storage_token_offset, int32_t causal_shift,
                            double softmax_scale, int32_t flags, int32_t dtype,
-                           int32_t quant_group_tokens, hipStream_t stream) {
+                           int32_t quant_group_tokens, hipStream_t stream, bool tiled_state) {
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
     set_error("sa_update_attention_state_int8: unsupported query dtype code %d", dtype);
     return SA_ERR_UNSUPPORTED_DTYPE;
@@ -1052,6 +1085,7 @@ int32_t launch_update_int8(const void* q, const void* k, const void* v, const vo
   p.sks_g = sks_g; p.sks_h = sks_h; p.svs_g = svs_g; p.svs_h = svs_h;
   p.scale_offset = storage_token_offset;
   p.scale_shift = shift;
+  p.tiled_state = tiled_state ? 1 : 0;
   const int dp = head_dim <= 32 ? 32 : head_dim <= 64 ? 64 : 128;
   const bool causal = (flags & SA_FLAG_CAUSAL) != 0;
   const bool init = (flags & SA_FLAG_INITIALIZE) != 0;
@@ -1086,7 +1120,8 @@ int32_t launch_transpose_v(const void* v, int64_t sv_t, int64_t sv_h, int32_t kv
 int32_t launch_finalize(const float* acc, const float* m, const float* l, void* out, float* lse,
                         int64_t sa_t, int64_t sa_h, int64_t ss_t, int64_t ss_h, int64_t so_t,
                         int64_t so_h, int64_t lse_sh, int64_t lse_off, int32_t q_tokens,
-                        int32_t q_heads, int32_t head_dim, int32_t dtype, hipStream_t stream) {
+                        int32_t q_heads, int32_t head_dim, int32_t dtype, hipStream_t stream,
+                        bool tiled_state) {
   if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
     set_error("sa_finalize_attention: unsupported dtype code %d", dtype);
     return SA_ERR_UNSUPPORTED_DTYPE;
@@ -1120,6 +1155,7 @@ int32_t launch_finalize(const float* acc, const float* m, const float* l, void* 
   p.lse_off = lse_off;
   p.groups = head_dim / 8;
   p.q_heads = q_heads;
+  p.tiled_state = tiled_state ? 1 : 0;
   p.total = (int64_t)q_tokens * q_heads * p.groups;
   const dim3 grid((unsigned)((p.total + 255) / 256));
   if (dtype == SA_DTYPE_BF16)

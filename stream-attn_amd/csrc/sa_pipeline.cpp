@@ -15,6 +15,11 @@
 // Copies are hipMemcpyAsync on two dedicated default-priority streams, so
 // PCIe traffic in both directions overlaps the kernels on the compute stream.
 //
+// The FP32 state (m, l, acc) of the pipeline is kept in the update kernel's
+// row-group layout (32-row groups in lane order), which the kernels and the
+// finalize of this file read and write; the buffers must therefore hold the
+// Q block's rows rounded up to a multiple of 32.
+//
 // Streamed chunks of a Q block of at least 512 rows are applied by two
 // launches, one per half of the block's rows: the first on the compute
 // stream, the second on the pipeline's own `side` stream (default priority).
@@ -255,7 +260,7 @@ int32_t launch_timed(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, 
                                  p->q_heads, 1, qt, p->head_dim, q_tokens, kv_tokens, p->q_heads,
                                  p->kv_heads, p->head_dim, q_local_offset, kv_local_offset,
                                  causal_shift, scale, flags, p->dtype, compute, merge_keys, fused,
-                                 v_transposed);
+                                 v_transposed, /*tiled_state=*/true);
   if (rc != 0) return rc;
   if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
   return 0;
@@ -283,7 +288,8 @@ int32_t launch_timed_int8(sa_pipeline* p, int slot, int32_t q_tokens, int32_t kv
       p->q_buffer, p->k_slots[slot], p->v_slots[slot], p->ks_slots[slot], p->vs_slots[slot], p->m,
       p->l, p->acc, qt, p->head_dim, kt, p->head_dim, kt, p->head_dim, p->kv_heads, 1, p->kv_heads, 1,
       p->q_heads, 1, qt, p->head_dim, q_tokens, kv_tokens, p->q_heads, p->kv_heads, p->head_dim,
-      q_local_offset, kv_local_offset, 0, causal_shift, scale, flags, p->dtype, 1, compute);
+      q_local_offset, kv_local_offset, 0, causal_shift, scale, flags, p->dtype, 1, compute,
+      /*tiled_state=*/true);
   if (rc != 0) return rc;
   if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], compute));
   return 0;
@@ -553,7 +559,7 @@ int32_t finalize(sa_pipeline* p, int32_t slot, int32_t q_tokens, float* lse, int
   const int64_t qt = (int64_t)p->q_heads * p->head_dim;
   return sa::launch_finalize(p->acc, p->m, p->l, dest, lse, qt, p->head_dim, p->q_heads, 1, qt,
                              p->head_dim, lse_sh, lse_off, q_tokens, p->q_heads, p->head_dim,
-                             p->dtype, compute);
+                             p->dtype, compute, /*tiled_state=*/true);
 }
 
 int32_t d2h(sa_pipeline* p, void* dst, const void* src, int64_t bytes, int32_t slot,
@@ -673,7 +679,8 @@ int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const ch
     {
       TraceRange range(p->trace, "seqattn:fused_finalize");
       rc = sa::launch_finalize(p->acc, p->m, p->l, buf[b], lse, q_stride, p->head_dim, p->q_heads, 1, q_stride,
-                               p->head_dim, lse_sh, ps.qt, ps.n, p->q_heads, p->head_dim, p->dtype, compute);
+                               p->head_dim, lse_sh, ps.qt, ps.n, p->q_heads, p->head_dim, p->dtype, compute,
+                               /*tiled_state=*/true);
       if (rc) return rc;
       SA_HIP_RETURN(hipEventRecord(p->alt_done[b], compute));
     }
@@ -1051,7 +1058,7 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
       }
       rc = sa::launch_finalize(p->acc, p->m, p->l, od + qs * stride_ot * 2, lse, qt_stride,
                                p->head_dim, p->q_heads, 1, stride_ot, stride_oh, lse_stride_h, qs,
-                               n, p->q_heads, p->head_dim, p->dtype, compute);
+                               n, p->q_heads, p->head_dim, p->dtype, compute, /*tiled_state=*/true);
       if (rc != 0) return rc;
       add_stats(stats, 0, 0, 1, 0, n);
     }
@@ -1088,7 +1095,7 @@ int32_t sa_pipeline_finalize_into(sa_pipeline* p, void* dest, int64_t stride_ot,
   const int64_t qt = (int64_t)p->q_heads * p->head_dim;
   return sa::launch_finalize(p->acc, p->m, p->l, dest, lse, qt, p->head_dim, p->q_heads, 1,
                              stride_ot, stride_oh, lse_stride_h, lse_token_offset, q_tokens,
-                             p->q_heads, p->head_dim, p->dtype, compute);
+                             p->q_heads, p->head_dim, p->dtype, compute, /*tiled_state=*/true);
 }
 
 int32_t sa_pipeline_release_q(sa_pipeline* p, void* compute_stream) {

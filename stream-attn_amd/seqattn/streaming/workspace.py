@@ -76,11 +76,13 @@ class CudaWorkspace:
             for _ in range(plan.num_kv_buffers)
         ]
         self.v = [torch.empty_like(t) for t in self.k]
-        self.running_max = torch.empty((plan.q_chunk_tokens, plan.q_heads), dtype=torch.float32, device=device)
+        # FP32 state rows rounded up to the kernel's 32-row groups: the
+        # pipeline stores the state group by group in the lanes' order.  The
+        # at most 31 extra rows come out of the planner's fixed margin.
+        state_rows = -(-plan.q_chunk_tokens // 32) * 32
+        self.running_max = torch.empty((state_rows, plan.q_heads), dtype=torch.float32, device=device)
         self.running_sum = torch.empty_like(self.running_max)
-        self.accumulator = torch.empty(
-            (plan.q_chunk_tokens, plan.q_heads, plan.head_dim), dtype=torch.float32, device=device
-        )
+        self.accumulator = torch.empty((state_rows, plan.q_heads, plan.head_dim), dtype=torch.float32, device=device)
         self.output = (
             [torch.empty_like(self.q) for _ in range(plan.num_output_buffers)]
             if plan.output_mode == "host"

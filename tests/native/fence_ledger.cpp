@@ -93,6 +93,10 @@ bool overlaps(const std::vector<Range>& a, const std::vector<Range>& b) {
 // `stride` elements of `elem` bytes.
 Range rows_of(const void* base, int64_t rows, int64_t stride, int elem) { return span(base, rows * stride * elem); }
 
+// Rows of pipeline state a launch over `rows` rows touches: whole 32-row
+// groups in the row-group layout.
+int64_t state_rows(int64_t rows, bool tiled) { return tiled ? (rows + 31) / 32 * 32 : rows; }
+
 // Per-head ranges of an LSE written for `rows` rows starting at token `off`.
 void lse_ranges(std::vector<Range>& out, const float* lse, int64_t sh, int64_t off, int64_t rows, int heads) {
   if (!lse) return;
@@ -160,7 +164,7 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
                       int64_t, int64_t sk_t, int64_t, int64_t sv_t, int64_t sv_h, int64_t ss_t, int64_t,
                       int64_t sa_t, int64_t, int32_t q_tokens, int32_t kv_tokens, int32_t q_heads,
                       int32_t kv_heads, int32_t, int32_t, int32_t, int32_t, double, int32_t flags, int32_t,
-                      hipStream_t stream, int32_t, const FusedOutput* fused, bool v_transposed) {
+                      hipStream_t stream, int32_t, const FusedOutput* fused, bool v_transposed, bool tiled) {
   Op op{kKernel, stream_id(stream), -1, {}, {}, "update"};
   op.reads.push_back(rows_of(q, q_tokens, sq_t, 2));
   op.reads.push_back(rows_of(k, kv_tokens, sk_t, 2));
@@ -169,8 +173,8 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
     op.writes.push_back(rows_of(fused->out, q_tokens, fused->so_t, 2));
     lse_ranges(op.writes, fused->lse, fused->lse_sh, fused->lse_off, q_tokens, q_heads);
   } else {
-    std::vector<Range> state = {rows_of(m, q_tokens, ss_t, 4), rows_of(l, q_tokens, ss_t, 4),
-                                rows_of(acc, q_tokens, sa_t, 4)};
+    const int64_t rows = state_rows(q_tokens, tiled);
+    std::vector<Range> state = {rows_of(m, rows, ss_t, 4), rows_of(l, rows, ss_t, 4), rows_of(acc, rows, sa_t, 4)};
     if (!(flags & SA_FLAG_INITIALIZE)) op.reads.insert(op.reads.end(), state.begin(), state.end());
     op.writes = state;
   }
@@ -190,12 +194,12 @@ int32_t launch_update_int8(const void* q, const void* k, const void* v, const vo
                            int64_t sv_t, int64_t, int64_t sks_g, int64_t, int64_t svs_g, int64_t, int64_t ss_t,
                            int64_t, int64_t sa_t, int64_t, int32_t q_tokens, int32_t kv_tokens, int32_t,
                            int32_t, int32_t, int32_t, int32_t, int32_t, int32_t, double, int32_t flags, int32_t,
-                           int32_t, hipStream_t stream) {
+                           int32_t, hipStream_t stream, bool tiled) {
   Op op{kKernel, stream_id(stream), -1, {}, {}, "update int8"};
   op.reads = {rows_of(q, q_tokens, sq_t, 2), rows_of(k, kv_tokens, sk_t, 1), rows_of(v, kv_tokens, sv_t, 1),
               rows_of(k_scales, kv_tokens, sks_g, 2), rows_of(v_scales, kv_tokens, svs_g, 2)};
-  std::vector<Range> state = {rows_of(m, q_tokens, ss_t, 4), rows_of(l, q_tokens, ss_t, 4),
-                              rows_of(acc, q_tokens, sa_t, 4)};
+  const int64_t rows = state_rows(q_tokens, tiled);
+  std::vector<Range> state = {rows_of(m, rows, ss_t, 4), rows_of(l, rows, ss_t, 4), rows_of(acc, rows, sa_t, 4)};
   if (!(flags & SA_FLAG_INITIALIZE)) op.reads.insert(op.reads.end(), state.begin(), state.end());
   op.writes = state;
   push(std::move(op));
@@ -204,9 +208,10 @@ int32_t launch_update_int8(const void* q, const void* k, const void* v, const vo
 
 int32_t launch_finalize(const float* acc, const float* m, const float* l, void* out, float* lse, int64_t sa_t,
                         int64_t, int64_t ss_t, int64_t, int64_t so_t, int64_t, int64_t lse_sh, int64_t lse_off,
-                        int32_t q_tokens, int32_t q_heads, int32_t, int32_t, hipStream_t stream) {
+                        int32_t q_tokens, int32_t q_heads, int32_t, int32_t, hipStream_t stream, bool tiled) {
   Op op{kKernel, stream_id(stream), -1, {}, {}, "finalize"};
-  op.reads = {rows_of(acc, q_tokens, sa_t, 4), rows_of(m, q_tokens, ss_t, 4), rows_of(l, q_tokens, ss_t, 4)};
+  const int64_t rows = state_rows(q_tokens, tiled);
+  op.reads = {rows_of(acc, rows, sa_t, 4), rows_of(m, rows, ss_t, 4), rows_of(l, rows, ss_t, 4)};
   op.writes = {rows_of(out, q_tokens, so_t, 2)};
   lse_ranges(op.writes, lse, lse_sh, lse_off, q_tokens, q_heads);
   push(std::move(op));

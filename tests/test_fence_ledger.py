@@ -77,9 +77,10 @@ class Pipeline:
         self.q_buffer = dev.take(q_chunk * q_row)
         k_slots = [dev.take(kv_chunk * kv_row) for _ in range(num_kv)]
         v_slots = [dev.take(kv_chunk * kv_row) for _ in range(num_kv)]
-        self.m = dev.take(q_chunk * q_heads * 4)
-        self.l = dev.take(q_chunk * q_heads * 4)
-        self.acc = dev.take(q_chunk * q_heads * head_dim * 4)
+        state_rows = -(-q_chunk // 32) * 32  # the pipeline's state is kept in 32-row groups
+        self.m = dev.take(state_rows * q_heads * 4)
+        self.l = dev.take(state_rows * q_heads * 4)
+        self.acc = dev.take(state_rows * q_heads * head_dim * 4)
         self.out_slots = [dev.take(q_chunk * q_row) for _ in range(num_out)] if out_slots else []
         self.device_space = dev
         self.q_row, self.kv_row, self.q_heads = q_row, kv_row, q_heads
