@@ -304,8 +304,9 @@ def main() -> int:
     value = flop / sec / 1e12
     h2d_per_step = stats.h2d_bytes / args.steps
     # Rows per pass: the plan's pass count with the rows spread evenly in
-    # multiples of 256 (the pipeline's schedule); one chunk span applies one
-    # K/V chunk to one pass's rows with two concurrent half-block launches.
+    # multiples of the kernel's workgroup tile (the pipeline's schedule); one
+    # chunk span applies one K/V chunk to one pass's rows with two concurrent
+    # half-block launches.
     rows_per_pass = stats.max_resident_q_tokens
     spans_per_step = stats.kv_tiles // args.steps
     busy_per_step_ms = busy_ms / args.steps

@@ -95,5 +95,9 @@ int32_t launch_finalize(const float* acc, const float* m, const float* l, void* 
                         int32_t q_heads, int32_t head_dim, int32_t dtype, hipStream_t stream,
                         bool tiled_state = false);
 // tiled_state: m, l and acc are the pipeline's own buffers in the row-group
-// layout (32-row groups, lane order; see the update kernel), not strided.
+// layout (16-row groups, lane order; see the update kernels), not strided.
+
+// Queries per workgroup of the update kernel for this head_dim: launches that
+// split a Q block split it at a multiple of this.
+int32_t update_block_rows(int32_t head_dim);
 }  // namespace sa

@@ -9,14 +9,16 @@
 // also writes LSE = (m + log2 l) * ln 2, which the reference does not produce.
 //
 // Update kernel work decomposition:
-//   head_dim 128: workgroup = 8 wavefronts (two per SIMD), each owning 32
-//   queries of one query head (256 queries per workgroup); while one wave of
-//   a SIMD waits on LDS or on the MFMA pipe the other issues.  Other head
-//   dims: 4 wavefronts (one per SIMD) owning QB blocks of 32 queries (QB = 2
-//   for head_dim <= 64, 1 for 256), so each K/V fragment read from LDS feeds
-//   QB MFMAs.  Workgroups are numbered head-major and dealt to the 8 XCDs in
-//   contiguous runs, so the workgroups resident on one XCD share one head's
-//   K/V stream in that XCD's L2.
+//   head_dim 72..128 (update48_kernel): workgroup = 8 wavefronts (two per
+//   SIMD), each owning 48 queries of one query head (384 queries per
+//   workgroup) as three 16-query blocks of 16x16x32 MFMAs; while one wave of
+//   a SIMD waits on LDS or on the MFMA pipe the other issues.  Head dims 16..64
+//   and 256 (update_kernel): 4 wavefronts (one per SIMD) owning QB blocks of
+//   32 queries (QB = 2 for head_dim <= 64, 1 for 256) with 32x32x16 MFMAs.
+//   Either way each K/V fragment read from LDS feeds several MFMAs.
+//   Workgroups are numbered head-major and dealt to the 8 XCDs in contiguous
+//   runs, so the workgroups resident on one XCD share one head's K/V stream in
+//   that XCD's L2.
 //   K/V stream through LDS in 64-key tiles, two stages: the tile after the one
 //   being computed is fetched by global_load_lds_dwordx4 (HBM/L2 -> LDS with
 //   no register staging) while the MFMAs run; one barrier per tile.
@@ -26,7 +28,8 @@
 //   (ds_read_b64_tr_b16, 4 consecutive keys per 16-lane group) free of bank
 //   conflicts.
 //
-// MFMA mapping (v_mfma_f32_32x32x16_{bf16,f16}: A 32x16, B 16x32, C 32x32):
+// MFMA mapping of update_kernel (v_mfma_f32_32x32x16_{bf16,f16}: A 32x16,
+// B 16x32, C 32x32; update48_kernel's 16x16x32 mapping is described there):
 //   S^T[key][query] = K . Q^T : A = K rows (LDS), B = Q fragments held in
 //   registers for the whole kernel.  In the C layout a lane owns one query
 //   column and 16 key rows, so softmax row reductions are in-lane.
@@ -148,17 +151,17 @@ struct UpdateParams {
   int32_t tiled_state = 0;
 };
 
-// Pipeline-owned FP32 state is kept in the order the update kernel's lanes
-// hold it.  Rows form groups of 32 (a wave's query block); group g of head h
-// is one block of 32 * head_dim floats (and 32 floats of m, of l) at block
-// index g * q_heads + h, so row r of a buffer sits where the token-major
-// layout would put it, rounded to its 32-row group.  Within a block, 4-float
-// chunk c (d = 4c .. 4c + 3) of row lr is at (c * 32 + lr) * 4: the 64 lanes
-// of a wave, (lr, hf) holding chunk 2 * (8 db + 2 g) / 2 + hf, read or write
-// 1 KB contiguously per instruction, where the strided layout touched 32
-// rows 28 KB apart with 32 bytes each.
+// Pipeline-owned FP32 state is kept in the order the update kernels' lanes
+// hold it.  Rows form groups of 16; group g of head h is one block of
+// 16 * head_dim floats (and 16 floats of m, of l) at block index
+// g * q_heads + h, so row r of a buffer sits where the token-major layout
+// would put it, rounded to its 16-row group.  Within a block, 4-float chunk c
+// (d = 4c .. 4c + 3) of row r is at (c * 16 + r) * 4.  A wave's state
+// instruction then covers whole 256-byte runs (16 rows of one chunk) where
+// the token-major layout touched one 16- or 32-byte piece per row, rows
+// q_heads * head_dim * 4 bytes apart.
 __device__ inline int64_t state_block(int64_t row, int head, int q_heads) {
-  return (row >> 5) * q_heads + head;
+  return (row >> 4) * q_heads + head;
 }
 
 // Row r (0..15) of a 32x32 C tile held in register i of a lane in half h.
@@ -179,11 +182,9 @@ template <int DP>
 struct Geometry {
   static constexpr int G = DP / 8;             // 16-byte granules per K/V row
   static constexpr int ROW_BYTES = DP * 2;
-  // head_dim 128: eight wavefronts (two per SIMD) of 32 queries; the second
-  // wave on a SIMD issues while the first waits on LDS or the MFMA pipe.
-  // Otherwise four wavefronts of 64 queries (32 for head_dim 256), each K/V
-  // fragment read from LDS feeding two MFMAs.
-  static constexpr int WAVES = DP == 128 ? 8 : 4;
+  // Four wavefronts of 64 queries (32 for head_dim 256), each K/V fragment
+  // read from LDS feeding two MFMAs.
+  static constexpr int WAVES = 4;
   static constexpr int THREADS = 64 * WAVES;
   static constexpr int QB = DP >= 128 ? 1 : 2;  // 32-query blocks per wave
   static constexpr int BLOCK_M = WAVES * 32 * QB;
@@ -192,9 +193,9 @@ struct Geometry {
   static constexpr int ROWS_PER_DMA = 1024 / ROW_BYTES;     // rows per wave-wide 1 KB DMA
   static constexpr int DMA_PER_WAVE = TILE_KEYS / ROWS_PER_DMA / WAVES;
   // K fragments requested ahead of their MFMAs, and V^T d-blocks per batch
-  // of transposing reads (bounded by the 256 VGPRs of an eight-wave kernel).
-  static constexpr int KB = DP == 128 ? 2 : DP / 16;
-  static constexpr int VB = DP == 128 ? 2 : (DP / 32 < 4 ? DP / 32 : 4);
+  // of transposing reads.
+  static constexpr int KB = DP / 16;
+  static constexpr int VB = DP / 32 < 4 ? DP / 32 : 4;
   static_assert(DMA_PER_WAVE >= 1, "tile too small for the workgroup");
   // INT8 staging: a tile is 64 rows of DP bytes; a wave-wide 16-byte-per-lane
   // DMA moves 1 KB, I8_GR granules of 16 int8 per row.
@@ -204,15 +205,10 @@ struct Geometry {
   static constexpr int I8_DMA_PER_WAVE = (I8_DMAS + WAVES - 1) / WAVES;
   static constexpr int I8_GRANULES = TILE_KEYS * I8_GR;               // per tensor per tile
   static constexpr int I8_PER_THREAD = (I8_GRANULES + THREADS - 1) / THREADS;
-  // Granule swizzle for gfx950's 64-bank LDS.  A ds_read_b128 phase is 16
-  // lanes (16 consecutive rows, one logical granule) and a ds_read_b64_tr_b16
-  // phase 32 lanes (4 consecutive rows, a 64-byte block of 4 granules).
-  // Head dim 128 (16 granules per 256-byte row): the mask is a bijection over
-  // 16 consecutive rows (the 16 b128 lanes hit 16 distinct granules) and rows
-  // r..r+3 (r % 4 == 0) differ in bits 2-3 (their 64-byte blocks land in
-  // distinct banks).  Narrower rows: 8 distinct masks over 8 rows.
+  // Granule swizzle: 8 distinct masks over 8 consecutive rows, so the K
+  // reads (ds_read_b128, consecutive rows at one logical granule) and the
+  // transposing V reads (4-row blocks) spread over the banks.
   __device__ static inline int swz(int row) {
-    if constexpr (G == 16) return ((row & 3) << 2) | ((row >> 2) & 3);
     return (((row & 3) << 1) | ((row >> 2) & 1)) & (G - 1);
   }
   __device__ static inline int offset(int row, int granule) {
@@ -220,16 +216,10 @@ struct Geometry {
   }
 };
 
-// VT: V arrives transposed per K/V head, [head_dim = 128 rows][keys], each
-// 16-key group stored in the order of the MFMA's k slots (keys 0-3, 8-11,
-// 4-7, 12-15; see transpose_v_kernel), padded with zero keys to a multiple of
-// 64.  p.sv_t is then the row stride and p.sv_h the head stride, in elements.
-// A lane's V^T fragment is one 16-byte LDS read instead of two transposing
-// 8-byte reads; the MFMA operands, and so the results, are the same.
-template <typename Op, int DP, bool CAUSAL, bool INIT, bool QUANT, bool VT = false>
+template <typename Op, int DP, bool CAUSAL, bool INIT, bool QUANT>
 __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const UpdateParams p) {
   using Geo = Geometry<DP>;
-  static_assert(!VT || (DP == 128 && !QUANT), "transposed V is read by the 16-bit head_dim 128 kernel only");
+  static_assert(DP != 128, "head_dim 128 runs update48_kernel");
   constexpr int QB = Geo::QB;
   constexpr int QC = DP / 16;  // 16-wide d slices of the QK^T contraction
   constexpr int DB = DP / 32;  // 32-row d blocks of the PV output
@@ -297,10 +287,11 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
     for (int d = 0; d < DB; ++d) acc[qb][d] = f32x16{};
     if (!INIT && qi[qb] < p.q_tokens) {
       const int64_t blk = state_block(qi[qb], head, p.q_heads);
-      const int64_t srow = p.tiled_state ? blk * 32 + lr : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+      const int r = qi[qb] & 15;
+      const int64_t srow = p.tiled_state ? blk * 16 + r : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
       m_run[qb] = p.m[srow];
       l_part[qb] = hf == 0 ? p.l[srow] : 0.f;
-      const float* arow = p.tiled_state ? p.acc + blk * 32 * p.head_dim + 4 * lr
+      const float* arow = p.tiled_state ? p.acc + blk * 16 * p.head_dim + 4 * r
                                         : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
@@ -308,7 +299,7 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
         for (int g = 0; g < 4; ++g) {
           const int col = 32 * d + 8 * g + 4 * hf;
           if (col < p.head_dim) {
-            const f32x4 v4 = *reinterpret_cast<const f32x4*>(arow + (p.tiled_state ? 32 * col : col));
+            const f32x4 v4 = *reinterpret_cast<const f32x4*>(arow + (p.tiled_state ? 16 * col : col));
             acc[qb][d][4 * g + 0] = v4[0];
             acc[qb][d][4 * g + 1] = v4[1];
             acc[qb][d][4 * g + 2] = v4[2];
@@ -350,19 +341,12 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
     dma_row[i] = row;
     k_off[i] = row * (int)p.sk_t + col;
     v_off[i] = row * (int)p.sv_t + col;
-    if constexpr (VT) {
-      // V^T tile: 128 rows of 64 keys (8 granules of 16 bytes); a 1 KB DMA
-      // moves 8 rows.  LDS granule g of row r holds key granule g ^ vswz(r).
-      const int vrow = chunk * 8 + lane / 8;
-      v_off[i] = vrow * (int)p.sv_t + (((lane % 8) ^ ((vrow >> 1) & 7)) * 8);
-    }
   }
   auto issue_tile = [&](int kt, uint8_t* stage) {
     uint8_t* k_stage = stage;
     uint8_t* v_stage = stage + Geo::TILE_BYTES;
     const uint16_t* kt_base = kp + (int64_t)kt * p.sk_t;
-    // Transposed V is padded with zero keys to whole tiles: no clamping.
-    const uint16_t* vt_base = VT ? vp + kt : vp + (int64_t)kt * p.sv_t;
+    const uint16_t* vt_base = vp + (int64_t)kt * p.sv_t;
     const bool tail = kt + Geo::TILE_KEYS > p.kv_tokens;
 #pragma unroll
     for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
@@ -371,7 +355,7 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
       if (tail && kt + dma_row[i] >= p.kv_tokens) {
         const int back = kt + dma_row[i] - (p.kv_tokens - 1);  // rows to step back
         ko -= back * (int)p.sk_t;
-        if constexpr (!VT) vo -= back * (int)p.sv_t;
+        vo -= back * (int)p.sv_t;
       }
       __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kt_base + ko),
                                        (SA_LDS void*)(k_stage + chunk * 1024), 16, 0, 0);
@@ -499,31 +483,17 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
         u32x4 vf[VB][2];
 #pragma unroll
         for (int dd = 0; dd < VB; ++dd) {
-          if constexpr (VT) {
-            // Row d = 32 (d0 + dd) + lr, k slots 8 hf .. 8 hf + 7 of the
-            // 16-key group rb / 16 + kc: one granule.
-            const int vrow = 32 * (d0 + dd) + lr;
+          const int granule = 4 * (d0 + dd) + 2 * (grp & 1) + ((gi & 3) >> 1);
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-              const int g = rb / 8 + 2 * kc + hf;
-              const uint32_t addr = v_lds + vrow * 128 + ((g ^ ((vrow >> 1) & 7)) << 4);
-              u32x4 w;
-              asm volatile("ds_read_b128 %0, %1" : "=v"(w) : "v"(addr));
-              vf[dd][kc] = w;
-            }
-          } else {
-            const int granule = 4 * (d0 + dd) + 2 * (grp & 1) + ((gi & 3) >> 1);
+          for (int kc = 0; kc < 2; ++kc) {
 #pragma unroll
-            for (int kc = 0; kc < 2; ++kc) {
-#pragma unroll
-              for (int r = 0; r < 2; ++r) {
-                const int row = rb + 16 * kc + 8 * r + 4 * (grp >> 1) + (gi >> 2);
-                const uint32_t addr = v_lds + Geo::offset(row, granule) + 8 * (gi & 1);
-                u32x2 w;
-                asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(addr));
-                vf[dd][kc][2 * r] = w[0];
-                vf[dd][kc][2 * r + 1] = w[1];
-              }
+            for (int r = 0; r < 2; ++r) {
+              const int row = rb + 16 * kc + 8 * r + 4 * (grp >> 1) + (gi >> 2);
+              const uint32_t addr = v_lds + Geo::offset(row, granule) + 8 * (gi & 1);
+              u32x2 w;
+              asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(w) : "v"(addr));
+              vf[dd][kc][2 * r] = w[0];
+              vf[dd][kc][2 * r + 1] = w[1];
             }
           }
         }
@@ -718,12 +688,13 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
       continue;
     }
     const int64_t blk = state_block(qi[qb], head, p.q_heads);
-    const int64_t srow = p.tiled_state ? blk * 32 + lr : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+    const int r = qi[qb] & 15;
+    const int64_t srow = p.tiled_state ? blk * 16 + r : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
     if (hf == 0) {
       p.m[srow] = m_run[qb];
       p.l[srow] = l_full;
     }
-    float* arow = p.tiled_state ? p.acc + blk * 32 * p.head_dim + 4 * lr
+    float* arow = p.tiled_state ? p.acc + blk * 16 * p.head_dim + 4 * r
                                 : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h;
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
@@ -733,9 +704,534 @@ __global__ __launch_bounds__(Geometry<DP>::THREADS) void update_kernel(const Upd
         if (col < p.head_dim) {
           const f32x4 v4 = {acc[qb][d][4 * g + 0], acc[qb][d][4 * g + 1], acc[qb][d][4 * g + 2],
                             acc[qb][d][4 * g + 3]};
-          *reinterpret_cast<f32x4*>(arow + (p.tiled_state ? 32 * col : col)) = v4;
+          *reinterpret_cast<f32x4*>(arow + (p.tiled_state ? 16 * col : col)) = v4;
         }
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// head_dim 72..128: 16x16x32 MFMAs, 48 queries per wavefront.
+//
+// Eight wavefronts (two per SIMD) own three 16-query blocks each, 384 queries
+// per workgroup.  Each K fragment and each V^T fragment read from LDS feeds
+// three MFMAs, so a 64-key tile costs two thirds of the LDS bytes per FLOP of
+// a 32-query wave, and the tile DMA feeds 384 queries instead of 256.  The
+// registers still fit two waves per SIMD: Q 48, O^T 96, S^T 24, P^T 12.
+//
+// v_mfma_f32_16x16x32_{bf16,f16}: A 16x32 (lane l: row l % 16, k 8 (l / 16)
+// .. +7), B 32x16 (lane l: column l % 16, k 8 (l / 16) .. +7), C 16x16 (lane
+// l: column l % 16, rows 4 (l / 16) .. +3).  With j = l / 16:
+//   S^T[key][query] = K . Q^T: A = K rows (LDS), B = Q (registers for the
+//   whole kernel).  The lane holds query l % 16 of each block and keys
+//   4j .. 4j + 3 of each 16-key block of the 32-key step.
+//   O^T[d][query] += V^T . P^T: B = P^T straight from those registers, k slot
+//   8j + e holding key 4j + e (e < 4) or 16 + 4j + e - 4; A = V^T rows in
+//   the same slot order, from two transposing LDS reads per fragment (or one
+//   16-byte read of the transposed copy of V).
+// A query's 32 keys of a step are spread over four lanes (j = 0..3); its
+// partial row sums stay per lane and are added in the fixed order
+// (l0 + l1) + (l2 + l3) wherever l is stored or merged.  The rescale rule
+// is the 32-query kernel's, decided per query from all four of its lanes.
+// In the row-group state layout the 64 lanes' chunks of one d block are 1 KB
+// of contiguous memory.
+struct Geometry48 {
+  static constexpr int DP = 128;
+  static constexpr int WAVES = 8;
+  static constexpr int THREADS = 64 * WAVES;
+  static constexpr int QB = 3;                                 // 16-query blocks per wave
+  static constexpr int BLOCK_M = WAVES * 16 * QB;              // 384
+  static constexpr int TILE_KEYS = 64;
+  static constexpr int TILE_BYTES = TILE_KEYS * DP * 2;        // K (or V) part of a stage
+  static constexpr int DMA_PER_WAVE = TILE_BYTES / 1024 / WAVES;
+  static constexpr int I8_TILE_BYTES = TILE_KEYS * DP;
+  static constexpr int I8_GR = DP / 16;
+  static constexpr int I8_DMAS = I8_TILE_BYTES / 1024;
+  static constexpr int I8_DMA_PER_WAVE = (I8_DMAS + WAVES - 1) / WAVES;
+  static constexpr int I8_GRANULES = TILE_KEYS * I8_GR;
+  static constexpr int I8_PER_THREAD = (I8_GRANULES + THREADS - 1) / THREADS;
+  static_assert(DMA_PER_WAVE >= 1 && I8_DMAS % WAVES == 0 && I8_GRANULES % THREADS == 0, "tile geometry");
+  // LDS layouts of one stage.  Every fragment read is a per-lane base plus a
+  // compile-time offset (the instruction's immediate), and every read is free
+  // of bank conflicts on the 64 four-byte banks.
+  //   K: four blocks of 32 d (64 keys x 64 bytes each).  Granule g (d 8g ..
+  //   8g + 7) of a key sits in block g / 4 at slot (g % 4) ^ ((key / 4) % 4):
+  //   the 16 lanes reading one granule of 16 consecutive keys cover 16
+  //   distinct bank groups.
+  //   V: eight blocks of 16 d (64 keys x 32 bytes each), unswizzled: the 32
+  //   lanes of a transposing read take 8 consecutive keys of one block, 256
+  //   contiguous bytes.
+  //   V^T (transposed copy): two blocks of 32 keys (128 d rows x 64 bytes
+  //   each), key granule kg of row r in block kg / 4 at slot
+  //   (kg % 4) ^ ((r / 4) % 4).
+  __device__ static inline int k_offset(int key, int g) {
+    return (g >> 2) * 4096 + key * 64 + (((g & 3) ^ ((key >> 2) & 3)) << 4);
+  }
+  __device__ static inline int v_offset(int key, int g) { return (g >> 1) * 2048 + key * 32 + ((g & 1) << 4); }
+  __device__ static inline int vt_offset(int row, int kg) {
+    return (kg >> 2) * 8192 + row * 64 + (((kg & 3) ^ ((row >> 2) & 3)) << 4);
+  }
+};
+
+template <typename Op>
+__device__ inline f32x4 mma16(u32x4 a, u32x4 b, f32x4 c);
+template <>
+__device__ inline f32x4 mma16<BF16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                 0, 0, 0);
+}
+template <>
+__device__ inline f32x4 mma16<FP16>(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                0, 0, 0);
+}
+
+// VT: V transposed per K/V head, [128 rows][keys], each 32-key group in the
+// k-slot order above (slot s holds key 16 ((s >> 2) & 1) + 4 (s >> 3) +
+// (s & 3)), zero keys up to a multiple of 64.
+template <typename Op, bool CAUSAL, bool INIT, bool QUANT, bool VT>
+__global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const UpdateParams p) {
+  using Geo = Geometry48;
+  static_assert(!(VT && QUANT), "transposed V is read by the 16-bit kernel only");
+  constexpr int QB = Geo::QB;
+
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_a[2 * Geo::TILE_BYTES];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_b[2 * Geo::TILE_BYTES];
+  constexpr int kStagingBytes = QUANT ? 2 * Geo::I8_TILE_BYTES : 16;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_qa[kStagingBytes];
+  __shared__ __attribute__((aligned(1024))) uint8_t lds_qb[kStagingBytes];
+
+  const int b = blockIdx.x;
+  const int logical = (b & 7) * p.xcd_run + (b >> 3);
+  if (logical >= p.q_blocks * p.q_heads) return;
+  const int head = logical / p.q_blocks;
+  const int qb_index = CAUSAL ? p.q_blocks - 1 - (logical - head * p.q_blocks) : logical - head * p.q_blocks;
+  const int q_block = qb_index * Geo::BLOCK_M;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int lane = tid & 63;
+  const int r16 = lane & 15;  // query within a 16-query block; key / d row within a 16-row fragment
+  const int j = lane >> 4;    // k-slot group
+  const int kv_head = head / p.group;
+  const int qw0 = q_block + wave * 16 * QB;
+
+  const uint16_t* qp = p.q + (int64_t)head * p.sq_h;
+  const uint16_t* kp = p.k + (int64_t)kv_head * p.sk_h;
+  const uint16_t* vp = p.v + (int64_t)kv_head * p.sv_h;
+
+  // Q fragments: query qw0 + 16 qb + r16, d = 32 c + 8 j .. +7.
+  u32x4 qf[QB][4];
+  int qi[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    qi[qb] = qw0 + 16 * qb + r16;
+    const bool ok = qi[qb] < p.q_tokens;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = 32 * c + 8 * j;
+      if (ok && d < p.head_dim)
+        qf[qb][c] = *reinterpret_cast<const u32x4*>(qp + (int64_t)qi[qb] * p.sq_t + d) ^ q_sign(p.scale_log2);
+      else
+        qf[qb][c] = u32x4{0, 0, 0, 0};
+    }
+  }
+
+  // Online-softmax state; acc[db][qb] holds d = 16 db + 4 j .. +3 of query qi[qb].
+  float m_run[QB], l_part[QB];
+  f32x4 acc[8][QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_part[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (!INIT && qi[qb] < p.q_tokens) {
+      const int64_t blk = state_block(qi[qb], head, p.q_heads);
+      const int64_t srow = p.tiled_state ? blk * 16 + r16 : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+      m_run[qb] = p.m[srow];
+      l_part[qb] = j == 0 ? p.l[srow] : 0.f;
+      const float* arow = p.tiled_state ? p.acc + blk * 16 * p.head_dim + 4 * lane
+                                        : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h + 4 * j;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        if (16 * db + 4 * j < p.head_dim)
+          acc[db][qb] = *reinterpret_cast<const f32x4*>(arow + (p.tiled_state ? 256 * db : 16 * db));
+      }
+    }
+  }
+
+  int kv_end = p.kv_tokens;
+  if (CAUSAL) {
+    const int q_last = min(p.q_tokens, q_block + Geo::BLOCK_M) - 1;
+    const int lim = p.q_local_offset + q_last + p.causal_shift - p.kv_local_offset + 1;
+    kv_end = max(0, min(kv_end, lim));
+  }
+  const int ntiles = (kv_end + Geo::TILE_KEYS - 1) / Geo::TILE_KEYS;
+  const float cf = scale_factor(p.scale_log2);
+
+  // HBM/L2 -> LDS DMA of key tile [kt, kt + 64).  A wave-wide DMA writes
+  // 1 KB of LDS linearly (16 bytes per lane), so each lane loads the global
+  // granule that the layouts above place at its LDS slot.  In the tail tile,
+  // keys past the chunk read its last key, and granules past head_dim read
+  // granule 0: finite values that are masked (keys) or multiplied by zero Q /
+  // never stored (d), with every address inside the caller's buffers.
+  int k_off[Geo::DMA_PER_WAVE], v_off[Geo::DMA_PER_WAVE], k_row[Geo::DMA_PER_WAVE], v_row[Geo::DMA_PER_WAVE];
+#pragma unroll
+  for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
+    const int slot = (wave * Geo::DMA_PER_WAVE + i) * 64 + lane;
+    {
+      const int key = (slot >> 2) & 63;
+      const int g = 4 * (slot >> 8) + ((slot & 3) ^ ((key >> 2) & 3));
+      k_row[i] = key;
+      k_off[i] = key * (int)p.sk_t + (8 * g < p.head_dim ? 8 * g : 0);
+    }
+    if constexpr (VT) {
+      const int row = (slot >> 2) & 127;
+      const int kg = 4 * (slot >> 9) + ((slot & 3) ^ ((row >> 2) & 3));
+      v_row[i] = 0;
+      v_off[i] = row * (int)p.sv_t + 8 * kg;
+    } else {
+      const int key = (slot >> 1) & 63;
+      const int g = 2 * (slot >> 7) + (slot & 1);
+      v_row[i] = key;
+      v_off[i] = key * (int)p.sv_t + (8 * g < p.head_dim ? 8 * g : 0);
+    }
+  }
+  auto issue_tile = [&](int kt, uint8_t* stage) {
+    uint8_t* k_stage = stage;
+    uint8_t* v_stage = stage + Geo::TILE_BYTES;
+    const uint16_t* kt_base = kp + (int64_t)kt * p.sk_t;
+    // Transposed V is padded with zero keys to whole tiles: no clamping.
+    const uint16_t* vt_base = VT ? vp + kt : vp + (int64_t)kt * p.sv_t;
+    const bool tail = kt + Geo::TILE_KEYS > p.kv_tokens;
+#pragma unroll
+    for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
+      const int chunk = wave * Geo::DMA_PER_WAVE + i;
+      int ko = k_off[i], vo = v_off[i];
+      if (tail) {
+        if (kt + k_row[i] >= p.kv_tokens) ko -= (kt + k_row[i] - (p.kv_tokens - 1)) * (int)p.sk_t;
+        if (!VT && kt + v_row[i] >= p.kv_tokens) vo -= (kt + v_row[i] - (p.kv_tokens - 1)) * (int)p.sv_t;
+      }
+      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kt_base + ko),
+                                       (SA_LDS void*)(k_stage + chunk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(vt_base + vo),
+                                       (SA_LDS void*)(v_stage + chunk * 1024), 16, 0, 0);
+    }
+  };
+
+  // Per-lane parts of the fragment addresses: K granule j of key r16 (of
+  // each 16-key block) and V^T granule j of row r16 share one form; the
+  // transposing V reads start at 8 bytes per lane.
+  const int k_lane = r16 * 64 + ((j ^ ((r16 >> 2) & 3)) << 4);
+  const int v_lane = VT ? k_lane : 8 * lane;
+
+  auto compute = [&](int t, const uint8_t* cur) {
+    const int kt = t * Geo::TILE_KEYS;
+    const uint8_t* k_stage = cur;
+    const uint8_t* v_stage = cur + Geo::TILE_BYTES;
+#pragma unroll
+    for (int sub = 0; sub < Geo::TILE_KEYS / kSubKeys; ++sub) {
+      const int rb = sub * kSubKeys;
+      const int key0 = kt + rb;
+
+      // S^T: two 16-key blocks x three 16-query blocks, four 32-wide d steps.
+      f32x4 s[2][QB];
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) s[kb][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        u32x4 kf[2];
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          kf[kb] = *reinterpret_cast<const u32x4*>(k_stage + k_lane + c * 4096 + (rb + 16 * kb) * 64);
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) s[kb][qb] = mma16<Op>(kf[kb], qf[qb][c], s[kb][qb]);
+      }
+
+      bool need_mask = key0 + kSubKeys > p.kv_tokens;
+      if (CAUSAL)
+        need_mask = need_mask || (p.kv_local_offset + key0 + kSubKeys - 1 >
+                                  p.q_local_offset + qw0 + p.causal_shift);
+      if (need_mask) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = key0 + 16 * kb + 4 * j + i;
+              bool ok = key < p.kv_tokens;
+              if (CAUSAL) ok = ok && (p.kv_local_offset + key <= p.q_local_offset + qi[qb] + p.causal_shift);
+              s[kb][qb][i] = ok ? s[kb][qb][i] : -INFINITY;
+            }
+      }
+
+      // P^T against the kept maximum, and the lane's partial row sum (8 keys).
+      auto exps = [&](int qb, float neg_m, u32x4& pq) -> float {
+        float sum = 0.f;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+          for (int e = 0; e < 2; ++e) {
+            const float p0 = __builtin_amdgcn_exp2f(fmaf(s[kb][qb][2 * e], cf, neg_m));
+            const float p1 = __builtin_amdgcn_exp2f(fmaf(s[kb][qb][2 * e + 1], cf, neg_m));
+            sum = (kb == 0 && e == 0) ? p0 + p1 : sum + (p0 + p1);
+            pq[2 * kb + e] = Op::pack2(p0, p1);
+          }
+        }
+        return sum;
+      };
+      u32x4 pf[QB];
+      float psum[QB];
+      bool grow[QB];
+      bool any = false;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        psum[qb] = exps(qb, m_run[qb] == -INFINITY ? 0.f : -m_run[qb], pf[qb]);
+        grow[qb] = !(psum[qb] <= 256.f) || m_run[qb] == -INFINITY;
+        any = any || grow[qb];
+      }
+      if (__ballot(any) != 0) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          // The query's own decision: one of its four lanes saw a partial sum
+          // above 2^8 (some logit may exceed m + 8) or it has no maximum yet.
+          const uint64_t bal = __ballot(grow[qb]);
+          uint32_t fold = (uint32_t)bal | (uint32_t)(bal >> 32);
+          fold |= fold >> 16;
+          const bool mine = (fold >> r16) & 1u;
+          float a = fmaxf(fmaxf(s[0][qb][0], s[0][qb][1]), fmaxf(s[0][qb][2], s[0][qb][3]));
+          a = fmaxf(a, fmaxf(fmaxf(s[1][qb][0], s[1][qb][1]), fmaxf(s[1][qb][2], s[1][qb][3]))) * cf;
+          float full = fmaxf(a, __shfl_xor(a, 16));
+          full = fmaxf(full, __shfl_xor(full, 32));
+          const float m_new = (mine && full > m_run[qb] + kRescaleThreshold) ? full : m_run[qb];
+          if (m_new != m_run[qb]) {
+            const float alpha = __builtin_amdgcn_exp2f(m_run[qb] - m_new);
+            l_part[qb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < 8; ++db) acc[db][qb] *= alpha;
+            m_run[qb] = m_new;
+            psum[qb] = exps(qb, -m_new, pf[qb]);
+          }
+        }
+      }
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) l_part[qb] += psum[qb];
+
+      // O^T += V^T P^T, two d blocks per batch of LDS reads.  The reads are
+      // inline asm with one explicit lgkmcnt wait, as in the 32-query kernel.
+      const uint32_t v_addr = (uint32_t)(uintptr_t)(const SA_LDS uint8_t*)(v_stage) + v_lane;
+#pragma unroll
+      for (int d0 = 0; d0 < 8; d0 += 2) {
+        u32x4 vf[2];
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) {
+          const int db = d0 + dd;
+          if constexpr (VT) {
+            // Rows d = 16 db + r16, key granule j of the step's 32-key block.
+            u32x4 w;
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(w) : "v"(v_addr), "i"((rb / 32) * 8192 + db * 1024));
+            vf[dd] = w;
+          } else {
+            // Lane (j, r16) addresses key 4 j + r16 / 4 of each 16-key block
+            // at d = 16 db + 4 (r16 % 4) .. +3; after the transpose it holds
+            // d = 16 db + r16 for keys 4 j .. 4 j + 3.
+#pragma unroll
+            for (int kb = 0; kb < 2; ++kb) {
+              u32x2 w;
+              asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2"
+                           : "=v"(w) : "v"(v_addr), "i"(db * 2048 + (rb + 16 * kb) * 32));
+              vf[dd][2 * kb] = w[0];
+              vf[dd][2 * kb + 1] = w[1];
+            }
+          }
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd) asm volatile("" : "+v"(vf[dd]));
+#pragma unroll
+        for (int dd = 0; dd < 2; ++dd)
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) acc[d0 + dd][qb] = mma16<Op>(vf[dd], pf[qb], acc[d0 + dd][qb]);
+      }
+    }
+  };
+
+  // Sum of a query's four partial row sums, identical on all four lanes.
+  auto full_l = [&](float x) -> float {
+    const float h = x + __shfl_xor(x, 16);
+    return h + __shfl_xor(h, 32);
+  };
+
+  if constexpr (!QUANT) {
+    int until_merge = p.merge_tiles;
+    auto tile = [&](int t, const uint8_t* cur, uint8_t* next) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (t + 1 < ntiles) issue_tile((t + 1) * Geo::TILE_KEYS, next);
+      compute(t, cur);
+      if (p.merge_tiles > 0 && --until_merge == 0) {
+        until_merge = p.merge_tiles;
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float full = full_l(l_part[qb]);
+          l_part[qb] = j == 0 ? full : 0.f;
+        }
+      }
+    };
+    if (ntiles > 0) issue_tile(0, lds_a);
+    for (int t = 0; t < ntiles; t += 2) {
+      tile(t, lds_a, lds_b);
+      if (t + 1 < ntiles) tile(t + 1, lds_b, lds_a);
+    }
+  } else {
+    const uint8_t* kp8 = reinterpret_cast<const uint8_t*>(p.k) + (int64_t)kv_head * p.sk_h;
+    const uint8_t* vp8 = reinterpret_cast<const uint8_t*>(p.v) + (int64_t)kv_head * p.sv_h;
+    int k8_off[Geo::I8_DMA_PER_WAVE], v8_off[Geo::I8_DMA_PER_WAVE], row8[Geo::I8_DMA_PER_WAVE];
+#pragma unroll
+    for (int i = 0; i < Geo::I8_DMA_PER_WAVE; ++i) {
+      const int chunk = wave + Geo::WAVES * i;
+      const int row = chunk * (1024 / Geo::DP) + lane / Geo::I8_GR;
+      const int gr = lane % Geo::I8_GR;
+      const int col = gr * 16 < p.head_dim ? gr * 16 : 0;
+      row8[i] = row;
+      k8_off[i] = row * (int)p.sk_t + col;
+      v8_off[i] = row * (int)p.sv_t + col;
+    }
+    auto issue_i8 = [&](int kt, uint8_t* stg) {
+      const uint8_t* kt_base = kp8 + (int64_t)kt * p.sk_t;
+      const uint8_t* vt_base = vp8 + (int64_t)kt * p.sv_t;
+#pragma unroll
+      for (int i = 0; i < Geo::I8_DMA_PER_WAVE; ++i) {
+        const int chunk = wave + Geo::WAVES * i;
+        int ko = k8_off[i], vo = v8_off[i];
+        if (kt + row8[i] >= p.kv_tokens) {
+          const int back = kt + row8[i] - (p.kv_tokens - 1);
+          ko -= back * (int)p.sk_t;
+          vo -= back * (int)p.sv_t;
+        }
+        __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kt_base + ko),
+                                         (SA_LDS void*)(stg + chunk * 1024), 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(vt_base + vo),
+                                         (SA_LDS void*)(stg + Geo::I8_TILE_BYTES + chunk * 1024), 16, 0, 0);
+      }
+    };
+    uint32_t ksc[Geo::I8_PER_THREAD], vsc[Geo::I8_PER_THREAD];
+    const uint16_t* ksp = p.ks + (int64_t)kv_head * p.sks_h;
+    const uint16_t* vsp = p.vs + (int64_t)kv_head * p.svs_h;
+    auto load_scales = [&](int kt) {
+#pragma unroll
+      for (int i = 0; i < Geo::I8_PER_THREAD; ++i) {
+        const int g = tid + Geo::THREADS * i;
+        const int key = min(kt + g / Geo::I8_GR, p.kv_tokens - 1);
+        const int64_t group = (int64_t)((p.scale_offset + key) >> p.scale_shift);
+        ksc[i] = ksp[group * p.sks_g];
+        vsc[i] = vsp[group * p.svs_g];
+      }
+    };
+    // dtype(fp32(k) * fp32(scale)) into the swizzled 16-bit stage, with the
+    // 32-query kernel's arithmetic.
+    auto dequant = [&](const uint8_t* stg, uint8_t* stage) {
+#pragma unroll
+      for (int i = 0; i < Geo::I8_PER_THREAD; ++i) {
+        const int g = tid + Geo::THREADS * i;
+        const int row = g / Geo::I8_GR;
+        const int gr = g % Geo::I8_GR;
+#pragma unroll
+        for (int tensor = 0; tensor < 2; ++tensor) {
+          const u32x4 raw = *reinterpret_cast<const u32x4*>(stg + tensor * Geo::I8_TILE_BYTES + row * Geo::DP + gr * 16);
+          const uint16_t bits = (uint16_t)(tensor == 0 ? ksc[i] : vsc[i]);
+          const float sc = (float)__builtin_bit_cast(_Float16, bits);
+          const float nb = -128.f * sc;
+          u32x4 out[2];
+#pragma unroll
+          for (int w = 0; w < 4; ++w) {
+            const uint32_t x = raw[w] ^ 0x80808080u;
+            const float f0 = fmaf((float)(x & 0xffu), sc, nb);
+            const float f1 = fmaf((float)((x >> 8) & 0xffu), sc, nb);
+            const float f2 = fmaf((float)((x >> 16) & 0xffu), sc, nb);
+            const float f3 = fmaf((float)(x >> 24), sc, nb);
+            out[w >> 1][2 * (w & 1)] = Op::pack2(f0, f1);
+            out[w >> 1][2 * (w & 1) + 1] = Op::pack2(f2, f3);
+          }
+          if (tensor == 0) {
+            *reinterpret_cast<u32x4*>(stage + Geo::k_offset(row, 2 * gr)) = out[0];
+            *reinterpret_cast<u32x4*>(stage + Geo::k_offset(row, 2 * gr + 1)) = out[1];
+          } else {
+            *reinterpret_cast<u32x4*>(stage + Geo::TILE_BYTES + Geo::v_offset(row, 2 * gr)) = out[0];
+            *reinterpret_cast<u32x4*>(stage + Geo::TILE_BYTES + Geo::v_offset(row, 2 * gr + 1)) = out[1];
+          }
+        }
+      }
+    };
+    auto tile_q = [&](int t, const uint8_t* cur, uint8_t* next, uint8_t* stg_cur, const uint8_t* stg_next) {
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (t + 2 < ntiles) issue_i8((t + 2) * Geo::TILE_KEYS, stg_cur);
+      if (t + 1 < ntiles) {
+        dequant(stg_next, next);
+        if (t + 2 < ntiles) load_scales((t + 2) * Geo::TILE_KEYS);
+      }
+      compute(t, cur);
+    };
+    if (ntiles > 0) {
+      issue_i8(0, lds_qa);
+      load_scales(0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      dequant(lds_qa, lds_a);
+      if (ntiles > 1) {
+        issue_i8(Geo::TILE_KEYS, lds_qb);
+        load_scales(Geo::TILE_KEYS);
+      }
+    }
+    for (int t = 0; t < ntiles; t += 2) {
+      tile_q(t, lds_a, lds_b, lds_qa, lds_qb);
+      if (t + 1 < ntiles) tile_q(t + 1, lds_b, lds_a, lds_qb, lds_qa);
+    }
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const float l_full = full_l(l_part[qb]);
+    if (qi[qb] >= p.q_tokens) continue;
+    if (p.out != nullptr) {
+      uint16_t* orow = p.out + (int64_t)qi[qb] * p.so_t + (int64_t)head * p.so_h + 4 * j;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        if (16 * db + 4 * j < p.head_dim) {
+          const f32x4& a = acc[db][qb];
+          u32x2 o = {0, 0};
+          if (l_full > 0.f) {
+            o[0] = Op::pack2(a[0] / l_full, a[1] / l_full);
+            o[1] = Op::pack2(a[2] / l_full, a[3] / l_full);
+          }
+          *reinterpret_cast<u32x2*>(orow + 16 * db) = o;
+        }
+      }
+      if (p.lse != nullptr && j == 0)
+        p.lse[(int64_t)head * p.lse_sh + p.lse_off + qi[qb]] =
+            l_full > 0.f ? (m_run[qb] + log2f(l_full)) * 0.69314718055994530942f : -INFINITY;
+      continue;
+    }
+    const int64_t blk = state_block(qi[qb], head, p.q_heads);
+    const int64_t srow = p.tiled_state ? blk * 16 + r16 : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+    if (j == 0) {
+      p.m[srow] = m_run[qb];
+      p.l[srow] = l_full;
+    }
+    float* arow = p.tiled_state ? p.acc + blk * 16 * p.head_dim + 4 * lane
+                                : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h + 4 * j;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) {
+      if (16 * db + 4 * j < p.head_dim)
+        *reinterpret_cast<f32x4*>(arow + (p.tiled_state ? 256 * db : 16 * db)) = acc[db][qb];
     }
   }
 }
@@ -761,15 +1257,15 @@ __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
   const int h = (int)(row % p.q_heads);
   const int64_t t = row / p.q_heads;
   const int64_t blk = state_block(t, h, p.q_heads);
-  const int lr = (int)(t & 31);
-  const int64_t srow = p.tiled_state ? blk * 32 + lr : t * p.ss_t + h * p.ss_h;
+  const int r = (int)(t & 15);
+  const int64_t srow = p.tiled_state ? blk * 16 + r : t * p.ss_t + h * p.ss_h;
   const float l = p.l[srow];
   f32x4 a0, a1;
   if (p.tiled_state) {
-    // Chunks 2g and 2g + 1 (d = 8g .. 8g + 7) of row lr.
-    const float* a = p.acc + blk * 32 * (p.groups * 8) + (2 * g * 32 + lr) * 4;
+    // Chunks 2g and 2g + 1 (d = 8g .. 8g + 7) of row r.
+    const float* a = p.acc + blk * 16 * (p.groups * 8) + (2 * g * 16 + r) * 4;
     a0 = *reinterpret_cast<const f32x4*>(a);
-    a1 = *reinterpret_cast<const f32x4*>(a + 32 * 4);
+    a1 = *reinterpret_cast<const f32x4*>(a + 16 * 4);
   } else {
     const float* a = p.acc + t * p.sa_t + h * p.sa_h + 8 * g;
     a0 = *reinterpret_cast<const f32x4*>(a);
@@ -792,13 +1288,14 @@ __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
   }
 }
 
-// Transposed copy of V for the VT update kernel.  V is [kv_tokens, kv_heads,
-// 128] with element strides (sv_t, sv_h); vt is [kv_heads][128][t_pad].  Key
-// k of a 16-key group goes to slot k with bits 2 and 3 swapped (slots 0-7
-// hold keys 0-3 and 8-11, slots 8-15 keys 4-7 and 12-15): the k-slot order in
-// which the update kernel's P^T operand holds the keys of a 32x32x16 MFMA, as
-// laid out by the S^T accumulator rows.  Keys kv_tokens .. t_pad-1 are zero.
-// One workgroup per (kv_head, 64 keys), staged through LDS.
+// Transposed copy of V for the head_dim-128 update kernel's VT variant.  V is
+// [kv_tokens, kv_heads, 128] with element strides (sv_t, sv_h); vt is
+// [kv_heads][128][t_pad].  Within each 32-key group, slot s holds key
+// 16 ((s >> 2) & 1) + 4 (s >> 3) + (s & 3): slots 8j .. 8j + 7 hold keys
+// 4j .. 4j + 3 and 16 + 4j .. 16 + 4j + 3, the k-slot order in which that
+// kernel's P^T operand holds the keys of a 16x16x32 MFMA, as laid out by the
+// S^T accumulator rows.  Keys kv_tokens .. t_pad-1 are zero.  One workgroup
+// per (kv_head, 64 keys), staged through LDS.
 struct TransposeParams {
   const uint16_t* v;
   uint16_t* vt;
@@ -833,8 +1330,8 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const TransposeParams 
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int sa = s0 + 8 * j + 2 * e, sb = sa + 1;
-        const int ka = (sa & ~12) | ((sa & 4) << 1) | ((sa & 8) >> 1);
-        const int kb = (sb & ~12) | ((sb & 4) << 1) | ((sb & 8) >> 1);
+        const int ka = (sa & 32) | (16 * ((sa >> 2) & 1) + 4 * ((sa >> 3) & 3) + (sa & 3));
+        const int kb = (sb & 32) | (16 * ((sb >> 2) & 1) + 4 * ((sb >> 3) & 3) + (sb & 3));
         w[e] = (uint32_t)tile[ka][d] | ((uint32_t)tile[kb][d] << 16);
       }
       *reinterpret_cast<u32x4*>(dst + 8 * j) = w;
@@ -842,33 +1339,63 @@ __global__ __launch_bounds__(256) void transpose_v_kernel(const TransposeParams 
   }
 }
 
-template <typename Op, int DP, bool QUANT, bool VT = false>
-hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t s) {
-  using Geo = Geometry<DP>;
+template <typename Op, bool QUANT, bool VT>
+hipError_t launch_update48(UpdateParams p, bool causal, bool init, hipStream_t s) {
+  using Geo = Geometry48;
   p.q_blocks = (p.q_tokens + Geo::BLOCK_M - 1) / Geo::BLOCK_M;
   const int64_t total = (int64_t)p.q_blocks * p.q_heads;
   p.xcd_run = (int32_t)((total + 7) / 8);
   const dim3 grid((unsigned)(8 * (int64_t)p.xcd_run));
+  const dim3 block(Geo::THREADS);
   if constexpr (VT) {
     // Transposed V serves launches that start the state (checked by the caller).
     if (causal)
-      hipLaunchKernelGGL((update_kernel<Op, DP, true, true, QUANT, true>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update48_kernel<Op, true, true, false, true>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((update_kernel<Op, DP, false, true, QUANT, true>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update48_kernel<Op, false, true, false, true>), grid, block, 0, s, p);
     return hipGetLastError();
   }
   if (causal) {
     if (init)
-      hipLaunchKernelGGL((update_kernel<Op, DP, true, true, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update48_kernel<Op, true, true, QUANT, false>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((update_kernel<Op, DP, true, false, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update48_kernel<Op, true, false, QUANT, false>), grid, block, 0, s, p);
   } else {
     if (init)
-      hipLaunchKernelGGL((update_kernel<Op, DP, false, true, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update48_kernel<Op, false, true, QUANT, false>), grid, block, 0, s, p);
     else
-      hipLaunchKernelGGL((update_kernel<Op, DP, false, false, QUANT>), grid, dim3(Geo::THREADS), 0, s, p);
+      hipLaunchKernelGGL((update48_kernel<Op, false, false, QUANT, false>), grid, block, 0, s, p);
   }
   return hipGetLastError();
+}
+
+// The 32-query kernel for head_dim 32, 64 and 256; head_dim 128 uses the
+// 48-query kernel.
+template <typename Op, int DP, bool QUANT, bool VT = false>
+hipError_t launch_update_dp(UpdateParams p, bool causal, bool init, hipStream_t s) {
+  if constexpr (DP == 128) {
+    return launch_update48<Op, QUANT, VT>(p, causal, init, s);
+  } else {
+    static_assert(!VT, "transposed V is read by the head_dim-128 kernel only");
+    using Geo = Geometry<DP>;
+    p.q_blocks = (p.q_tokens + Geo::BLOCK_M - 1) / Geo::BLOCK_M;
+    const int64_t total = (int64_t)p.q_blocks * p.q_heads;
+    p.xcd_run = (int32_t)((total + 7) / 8);
+    const dim3 grid((unsigned)(8 * (int64_t)p.xcd_run));
+    const dim3 block(Geo::THREADS);
+    if (causal) {
+      if (init)
+        hipLaunchKernelGGL((update_kernel<Op, DP, true, true, QUANT>), grid, block, 0, s, p);
+      else
+        hipLaunchKernelGGL((update_kernel<Op, DP, true, false, QUANT>), grid, block, 0, s, p);
+    } else {
+      if (init)
+        hipLaunchKernelGGL((update_kernel<Op, DP, false, true, QUANT>), grid, block, 0, s, p);
+      else
+        hipLaunchKernelGGL((update_kernel<Op, DP, false, false, QUANT>), grid, block, 0, s, p);
+    }
+    return hipGetLastError();
+  }
 }
 
 template <typename Op>
@@ -897,6 +1424,11 @@ inline bool aligned(const void* ptr, uintptr_t n) { return (reinterpret_cast<uin
 }  // namespace
 
 namespace sa {
+
+int32_t update_block_rows(int32_t head_dim) {
+  if (head_dim > 64 && head_dim <= 128) return Geometry48::BLOCK_M;
+  return head_dim <= 64 ? Geometry<64>::BLOCK_M : Geometry<256>::BLOCK_M;
+}
 
 int32_t launch_update(const void* q, const void* k, const void* v, float* m, float* l, float* acc,
                       int64_t sq_t, int64_t sq_h, int64_t sk_t, int64_t sk_h, int64_t sv_t,

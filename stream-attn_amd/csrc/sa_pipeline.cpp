@@ -16,9 +16,9 @@
 // PCIe traffic in both directions overlaps the kernels on the compute stream.
 //
 // The FP32 state (m, l, acc) of the pipeline is kept in the update kernel's
-// row-group layout (32-row groups in lane order), which the kernels and the
+// row-group layout (16-row groups in lane order), which the kernels and the
 // finalize of this file read and write; the buffers must therefore hold the
-// Q block's rows rounded up to a multiple of 32.
+// Q block's rows rounded up to a multiple of 16.
 //
 // Streamed chunks of a Q block of at least 512 rows are applied by two
 // launches, one per half of the block's rows: the first on the compute
@@ -344,8 +344,9 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
   if (causal) visible_end = std::max<int64_t>(0, (int64_t)q_local_offset + q_tokens + causal_shift);
   const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
   // Rows [0, split) update on the compute stream, [split, q_tokens) on side;
-  // split is a multiple of 256 queries, the workgroup tile.
-  const int32_t split = (!src.on_device && q_tokens >= 512) ? (q_tokens / 2 + 255) / 256 * 256 : q_tokens;
+  // split is a multiple of the kernel's workgroup tile.
+  const int32_t tile = sa::update_block_rows(p->head_dim);
+  const int32_t split = (!src.on_device && q_tokens >= 2 * tile) ? (q_tokens / 2 + tile - 1) / tile * tile : q_tokens;
   const bool two = split < q_tokens && kv_tokens > 0;
   const char* q_second = static_cast<const char*>(q) + (int64_t)split * sq_t * 2;
   SideJoin join{p, compute};
@@ -591,16 +592,16 @@ struct Pass {
 
 // Rows per pass for a segment of q_length query rows: the pass count of
 // q_chunk-row blocks, with the rows spread evenly over the passes in
-// multiples of 256 queries (the update kernel's workgroup tile) instead of a
-// short last block.  A short pass applies every K/V chunk to few rows, so its
+// multiples of the update kernel's workgroup tile instead of a short last
+// block.  A short pass applies every K/V chunk to few rows, so its
 // chunk copies outrun its kernels; even passes keep each chunk's copy hidden
 // behind its compute.  The pass count, and with it the H2D bytes, is that of
 // q_chunk-row blocks.
-int64_t pass_rows(int64_t q_length, int32_t q_chunk) {
+int64_t pass_rows(int64_t q_length, int32_t q_chunk, int32_t tile) {
   if (q_length <= q_chunk) return q_chunk;
   const int64_t passes = (q_length + q_chunk - 1) / q_chunk;
   const int64_t even = (q_length + passes - 1) / passes;
-  return std::min<int64_t>(q_chunk, (even + 255) / 256 * 256);
+  return std::min<int64_t>(q_chunk, (even + tile - 1) / tile * tile);
 }
 
 // sa_pipeline_run with one output slot.  The plan's two block-sized buffers
@@ -1031,7 +1032,7 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
                         softmax_scale, (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, p->kv_chunk,
                         &fused, 0, vt);
       if (rc != 0) return rc;
-      const int64_t block = pass_rows(q_length, p->q_chunk);
+      const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
       for (int64_t qs = q_start; qs < q_stop; qs += block) {
         const int64_t n = std::min<int64_t>(block, q_stop - qs);
         const int64_t visible_end = causal ? std::max<int64_t>(0, qs - q_start + n + causal_shift) : INT64_MAX;
@@ -1241,7 +1242,7 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
         sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
         return SA_ERR_INVALID_ARGUMENT;
       }
-      const int64_t block = pass_rows(q_length, p->q_chunk);
+      const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
       for (int64_t qt = q_start; qt < q_stop; qt += block)
         passes.push_back(Pass{qt, k_start, (int32_t)std::min<int64_t>(block, q_stop - qt), (int32_t)k_length,
                               (int32_t)(qt - q_start), (int32_t)(k_length - q_length)});
@@ -1258,7 +1259,7 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
       return SA_ERR_INVALID_ARGUMENT;
     }
     const int32_t causal_shift = (int32_t)(k_length - q_length);
-    const int64_t block = pass_rows(q_length, p->q_chunk);
+    const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
     for (int64_t qt = q_start; qt < q_stop; qt += block) {
       const int32_t n = (int32_t)std::min<int64_t>(block, q_stop - qt);
       int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);

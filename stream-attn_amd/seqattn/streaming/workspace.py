@@ -76,10 +76,10 @@ class CudaWorkspace:
             for _ in range(plan.num_kv_buffers)
         ]
         self.v = [torch.empty_like(t) for t in self.k]
-        # FP32 state rows rounded up to the kernel's 32-row groups: the
+        # FP32 state rows rounded up to the kernels' 16-row groups: the
         # pipeline stores the state group by group in the lanes' order.  The
-        # at most 31 extra rows come out of the planner's fixed margin.
-        state_rows = -(-plan.q_chunk_tokens // 32) * 32
+        # at most 15 extra rows come out of the planner's fixed margin.
+        state_rows = -(-plan.q_chunk_tokens // 16) * 16
         self.running_max = torch.empty((state_rows, plan.q_heads), dtype=torch.float32, device=device)
         self.running_sum = torch.empty_like(self.running_max)
         self.accumulator = torch.empty((state_rows, plan.q_heads, plan.head_dim), dtype=torch.float32, device=device)

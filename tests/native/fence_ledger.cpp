@@ -93,9 +93,9 @@ bool overlaps(const std::vector<Range>& a, const std::vector<Range>& b) {
 // `stride` elements of `elem` bytes.
 Range rows_of(const void* base, int64_t rows, int64_t stride, int elem) { return span(base, rows * stride * elem); }
 
-// Rows of pipeline state a launch over `rows` rows touches: whole 32-row
+// Rows of pipeline state a launch over `rows` rows touches: whole 16-row
 // groups in the row-group layout.
-int64_t state_rows(int64_t rows, bool tiled) { return tiled ? (rows + 31) / 32 * 32 : rows; }
+int64_t state_rows(int64_t rows, bool tiled) { return tiled ? (rows + 15) / 16 * 16 : rows; }
 
 // Per-head ranges of an LSE written for `rows` rows starting at token `off`.
 void lse_ranges(std::vector<Range>& out, const float* lse, int64_t sh, int64_t off, int64_t rows, int heads) {
@@ -159,6 +159,12 @@ hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKin
 
 // ------------------------------------------------------- kernel launchers
 namespace sa {
+
+// Same values as the kernels' workgroup tiles.
+int32_t update_block_rows(int32_t head_dim) {
+  if (head_dim > 64 && head_dim <= 128) return 384;
+  return head_dim <= 64 ? 256 : 128;
+}
 
 int32_t launch_update(const void* q, const void* k, const void* v, float* m, float* l, float* acc, int64_t sq_t,
                       int64_t, int64_t sk_t, int64_t, int64_t sv_t, int64_t sv_h, int64_t ss_t, int64_t,

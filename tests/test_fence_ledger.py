@@ -77,7 +77,7 @@ class Pipeline:
         self.q_buffer = dev.take(q_chunk * q_row)
         k_slots = [dev.take(kv_chunk * kv_row) for _ in range(num_kv)]
         v_slots = [dev.take(kv_chunk * kv_row) for _ in range(num_kv)]
-        state_rows = -(-q_chunk // 32) * 32  # the pipeline's state is kept in 32-row groups
+        state_rows = -(-q_chunk // 16) * 16  # the pipeline's state is kept in 16-row groups
         self.m = dev.take(state_rows * q_heads * 4)
         self.l = dev.take(state_rows * q_heads * 4)
         self.acc = dev.take(state_rows * q_heads * head_dim * 4)
