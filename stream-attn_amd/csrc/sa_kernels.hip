@@ -754,24 +754,21 @@ struct Geometry48 {
   static_assert(DMA_PER_WAVE >= 1 && I8_DMAS % WAVES == 0 && I8_GRANULES % THREADS == 0, "tile geometry");
   // LDS layouts of one stage.  Every fragment read is a per-lane base plus a
   // compile-time offset (the instruction's immediate), and every read is free
-  // of bank conflicts on the 64 four-byte banks.
-  //   K: four blocks of 32 d (64 keys x 64 bytes each).  Granule g (d 8g ..
-  //   8g + 7) of a key sits in block g / 4 at slot (g % 4) ^ ((key / 4) % 4):
-  //   the 16 lanes reading one granule of 16 consecutive keys cover 16
-  //   distinct bank groups.
-  //   V: eight blocks of 16 d (64 keys x 32 bytes each), unswizzled: the 32
-  //   lanes of a transposing read take 8 consecutive keys of one block, 256
-  //   contiguous bytes.
-  //   V^T (transposed copy): two blocks of 32 keys (128 d rows x 64 bytes
-  //   each), key granule kg of row r in block kg / 4 at slot
-  //   (kg % 4) ^ ((r / 4) % 4).
+  // of bank conflicts (measured with SQ_LDS_BANK_CONFLICT).
+  //   K: in fragment order.  The 16-key x 32-d A fragment (16-key block kb,
+  //   d block c) is 1 KB at (4 kb + c) KB, lane (j, r16)'s 16 bytes (key
+  //   16 kb + r16, d 32 c + 8 j .. +7) at 16 * lane: each read is 1 KB of
+  //   consecutive bytes.
+  //   V: eight blocks of 16 d (64 keys x 32 bytes each).  A transposing read
+  //   has each 16-lane group take 4 consecutive keys (128 bytes) of a block:
+  //   512 consecutive bytes per read.
+  //   V^T (transposed copy): in fragment order, the 16-d x 32-key fragment
+  //   (32-key block sb, d block db) at (8 sb + db) KB, lane (j, r16)'s 16
+  //   bytes (row 16 db + r16, key granule 4 sb + j) at 16 * lane.
   __device__ static inline int k_offset(int key, int g) {
-    return (g >> 2) * 4096 + key * 64 + (((g & 3) ^ ((key >> 2) & 3)) << 4);
+    return ((key >> 4) * 4 + (g >> 2)) * 1024 + 16 * (((g & 3) << 4) | (key & 15));
   }
   __device__ static inline int v_offset(int key, int g) { return (g >> 1) * 2048 + key * 32 + ((g & 1) << 4); }
-  __device__ static inline int vt_offset(int row, int kg) {
-    return (kg >> 2) * 8192 + row * 64 + (((kg & 3) ^ ((row >> 2) & 3)) << 4);
-  }
 };
 
 template <typename Op>
@@ -882,14 +879,16 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
   for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
     const int slot = (wave * Geo::DMA_PER_WAVE + i) * 64 + lane;
     {
-      const int key = (slot >> 2) & 63;
-      const int g = 4 * (slot >> 8) + ((slot & 3) ^ ((key >> 2) & 3));
+      // Fragment slot >> 6 = 4 kb + c, lane slot & 63 = 16 j + r16.
+      const int key = 16 * (slot >> 8) + (slot & 15);
+      const int g = 4 * ((slot >> 6) & 3) + ((slot >> 4) & 3);
       k_row[i] = key;
       k_off[i] = key * (int)p.sk_t + (8 * g < p.head_dim ? 8 * g : 0);
     }
     if constexpr (VT) {
-      const int row = (slot >> 2) & 127;
-      const int kg = 4 * (slot >> 9) + ((slot & 3) ^ ((row >> 2) & 3));
+      // Fragment slot >> 6 = 8 sb + db, lane slot & 63 = 16 j + r16.
+      const int row = 16 * ((slot >> 6) & 7) + (slot & 15);
+      const int kg = 4 * (slot >> 9) + ((slot >> 4) & 3);
       v_row[i] = 0;
       v_off[i] = row * (int)p.sv_t + 8 * kg;
     } else {
@@ -921,11 +920,10 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
     }
   };
 
-  // Per-lane parts of the fragment addresses: K granule j of key r16 (of
-  // each 16-key block) and V^T granule j of row r16 share one form; the
-  // transposing V reads start at 8 bytes per lane.
-  const int k_lane = r16 * 64 + ((j ^ ((r16 >> 2) & 3)) << 4);
-  const int v_lane = VT ? k_lane : 8 * lane;
+  // Per-lane parts of the fragment addresses: 16 bytes per lane for the K and
+  // V^T fragments, 8 bytes per lane for the transposing V reads.
+  const int k_lane = 16 * lane;
+  const int v_lane = VT ? 16 * lane : 8 * lane;
 
   auto compute = [&](int t, const uint8_t* cur) {
     const int kt = t * Geo::TILE_KEYS;
@@ -947,7 +945,7 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
         u32x4 kf[2];
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
-          kf[kb] = *reinterpret_cast<const u32x4*>(k_stage + k_lane + c * 4096 + (rb + 16 * kb) * 64);
+          kf[kb] = *reinterpret_cast<const u32x4*>(k_stage + k_lane + ((rb / 16 + kb) * 4 + c) * 1024);
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -994,6 +992,8 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
 #pragma unroll
       for (int qb = 0; qb < QB; ++qb) {
         psum[qb] = exps(qb, m_run[qb] == -INFINITY ? 0.f : -m_run[qb], pf[qb]);
+        // Every p <= 2^8 (no logit above m + 8) whenever the lane's sum is;
+        // a row without a maximum yet always takes the rescale path.
         grow[qb] = !(psum[qb] <= 256.f) || m_run[qb] == -INFINITY;
         any = any || grow[qb];
       }
@@ -1036,7 +1036,7 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
           if constexpr (VT) {
             // Rows d = 16 db + r16, key granule j of the step's 32-key block.
             u32x4 w;
-            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(w) : "v"(v_addr), "i"((rb / 32) * 8192 + db * 1024));
+            asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(w) : "v"(v_addr), "i"(((rb / 32) * 8 + db) * 1024));
             vf[dd] = w;
           } else {
             // Lane (j, r16) addresses key 4 j + r16 / 4 of each 16-key block
