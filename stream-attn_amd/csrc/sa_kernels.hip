@@ -807,7 +807,7 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
   const int q_block = qb_index * Geo::BLOCK_M;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int r16 = lane & 15;  // query within a 16-query block; key / d row within a 16-row fragment
   const int j = lane >> 4;    // k-slot group
@@ -868,55 +868,64 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
   const int ntiles = (kv_end + Geo::TILE_KEYS - 1) / Geo::TILE_KEYS;
   const float cf = scale_factor(p.scale_log2);
 
-  // HBM/L2 -> LDS DMA of key tile [kt, kt + 64).  A wave-wide DMA writes
-  // 1 KB of LDS linearly (16 bytes per lane), so each lane loads the global
-  // granule that the layouts above place at its LDS slot.  In the tail tile,
-  // keys past the chunk read its last key, and granules past head_dim read
-  // granule 0: finite values that are masked (keys) or multiplied by zero Q /
-  // never stored (d), with every address inside the caller's buffers.
-  int k_off[Geo::DMA_PER_WAVE], v_off[Geo::DMA_PER_WAVE], k_row[Geo::DMA_PER_WAVE], v_row[Geo::DMA_PER_WAVE];
-#pragma unroll
-  for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
-    const int slot = (wave * Geo::DMA_PER_WAVE + i) * 64 + lane;
-    {
-      // Fragment slot >> 6 = 4 kb + c, lane slot & 63 = 16 j + r16.
-      const int key = 16 * (slot >> 8) + (slot & 15);
-      const int g = 4 * ((slot >> 6) & 3) + ((slot >> 4) & 3);
-      k_row[i] = key;
-      k_off[i] = key * (int)p.sk_t + (8 * g < p.head_dim ? 8 * g : 0);
-    }
-    if constexpr (VT) {
-      // Fragment slot >> 6 = 8 sb + db, lane slot & 63 = 16 j + r16.
-      const int row = 16 * ((slot >> 6) & 7) + (slot & 15);
-      const int kg = 4 * (slot >> 9) + ((slot >> 4) & 3);
-      v_row[i] = 0;
-      v_off[i] = row * (int)p.sv_t + 8 * kg;
-    } else {
-      const int key = (slot >> 1) & 63;
-      const int g = 2 * (slot >> 7) + (slot & 1);
-      v_row[i] = key;
-      v_off[i] = key * (int)p.sv_t + (8 * g < p.head_dim ? 8 * g : 0);
-    }
-  }
+  // HBM/L2 -> LDS DMA of key tile [kt, kt + 64), issued by waves 0-3 (the
+  // first wave of each SIMD) only.  The second waves of the SIMDs get the
+  // smaller share of issue slots while both compute, so they finish a tile
+  // last; the first waves wait at the tile barrier meanwhile, and issuing
+  // the DMA there takes it off the tile's critical path.
+  // A wave-wide DMA writes 1 KB of LDS linearly (16 bytes per lane); piece f
+  // (0..15) of a tensor is LDS bytes [f KB, f KB + 1 KB), and each lane loads
+  // the global granule the layouts above place at its slot.  The global
+  // element offset is a wave-uniform part (f) plus a per-lane part (lane):
+  //   K (fragment 4 kb + c = f): key 16 (f / 4) + lane % 16, d 32 (f % 4) + 8 (lane / 16);
+  //   V: key (32 f) % 64 + lane / 2, d 16 (f / 2) + 8 (lane % 2);
+  //   V^T (fragment 8 sb + db = f): row 16 (f % 8) + lane % 16,
+  //   key 32 (f / 8) + 8 (lane / 16).
+  // In the tail tile, keys past the chunk read its last key, and V^T keys
+  // past the row's padded length read the row's first granule; granules
+  // past head_dim read d = 0.  Those values are finite and masked (keys) or
+  // multiplied by zero Q / never stored (d), and every address stays inside
+  // the caller's buffers.
+  constexpr int kPieces = Geo::TILE_BYTES / 1024;   // per tensor per tile
+  constexpr int kIssuers = 4;
+  const int k_dma_lane = (lane & 15) * (int)p.sk_t + 8 * (lane >> 4);
+  const int v_dma_lane = VT ? (lane & 15) * (int)p.sv_t + 8 * (lane >> 4) : (lane >> 1) * (int)p.sv_t + 8 * (lane & 1);
   auto issue_tile = [&](int kt, uint8_t* stage) {
+    if (wave >= kIssuers) return;
     uint8_t* k_stage = stage;
     uint8_t* v_stage = stage + Geo::TILE_BYTES;
-    const uint16_t* kt_base = kp + (int64_t)kt * p.sk_t;
-    // Transposed V is padded with zero keys to whole tiles: no clamping.
-    const uint16_t* vt_base = VT ? vp + kt : vp + (int64_t)kt * p.sv_t;
     const bool tail = kt + Geo::TILE_KEYS > p.kv_tokens;
+    const bool narrow = p.head_dim < 128;
 #pragma unroll
-    for (int i = 0; i < Geo::DMA_PER_WAVE; ++i) {
-      const int chunk = wave * Geo::DMA_PER_WAVE + i;
-      int ko = k_off[i], vo = v_off[i];
+    for (int i = 0; i < kPieces / kIssuers; ++i) {
+      const int f = wave * (kPieces / kIssuers) + i;
+      const int k_key0 = 16 * (f >> 2);
+      const int k_d0 = 32 * (f & 3);
+      int ko = k_dma_lane;
+      if (narrow && k_d0 + 8 * (lane >> 4) >= p.head_dim) ko -= k_d0 + 8 * (lane >> 4);
       if (tail) {
-        if (kt + k_row[i] >= p.kv_tokens) ko -= (kt + k_row[i] - (p.kv_tokens - 1)) * (int)p.sk_t;
-        if (!VT && kt + v_row[i] >= p.kv_tokens) vo -= (kt + v_row[i] - (p.kv_tokens - 1)) * (int)p.sv_t;
+        const int key = kt + k_key0 + (lane & 15);
+        if (key >= p.kv_tokens) ko -= (key - (p.kv_tokens - 1)) * (int)p.sk_t;
       }
-      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kt_base + ko),
-                                       (SA_LDS void*)(k_stage + chunk * 1024), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(vt_base + vo),
-                                       (SA_LDS void*)(v_stage + chunk * 1024), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(kp + (int64_t)(kt + k_key0) * p.sk_t + k_d0 + ko),
+                                       (SA_LDS void*)(k_stage + f * 1024), 16, 0, 0);
+      const uint16_t* vb;
+      int vo = v_dma_lane;
+      if constexpr (VT) {
+        const int row0 = 16 * (f & 7), key0 = 32 * (f >> 3);
+        vb = vp + (int64_t)row0 * p.sv_t + kt + key0;
+        if (tail && kt + key0 + 8 * (lane >> 4) >= p.sv_t) vo -= kt + key0 + 8 * (lane >> 4);
+      } else {
+        const int v_key0 = (32 * f) & (Geo::TILE_KEYS - 1);
+        const int v_d0 = 16 * ((32 * f) / Geo::TILE_KEYS);
+        vb = vp + (int64_t)(kt + v_key0) * p.sv_t + v_d0;
+        if (narrow && v_d0 + 8 * (lane & 1) >= p.head_dim) vo -= v_d0 + 8 * (lane & 1);
+        if (tail) {
+          const int key = kt + v_key0 + (lane >> 1);
+          if (key >= p.kv_tokens) vo -= (key - (p.kv_tokens - 1)) * (int)p.sv_t;
+        }
+      }
+      __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(vb + vo), (SA_LDS void*)(v_stage + f * 1024), 16, 0, 0);
     }
   };
 
