@@ -39,8 +39,9 @@ class StreamingAttentionConfig:
     # setting any one switches to the portable 64x64/4/2 baseline with the
     # supplied values as overrides.  block_m / block_n set the alignment of the
     # planned Q and K/V chunks; the gfx950 kernel's own tile geometry is fixed
-    # (256 queries x 64 keys per workgroup for head_dim <= 128, K/V tiles
-    # double-buffered in LDS).
+    # (64 keys per tile; 384 queries per workgroup for head_dim 72-128, 256
+    # for head_dim <= 64 and 128 for head_dim 256; K/V tiles double-buffered
+    # in LDS).
     block_m: int | None = None
     block_n: int | None = None
     num_warps: int | None = None

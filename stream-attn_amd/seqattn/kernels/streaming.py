@@ -4,8 +4,8 @@
 the reference wrappers (src/seqattn_core/kernels/streaming.py:205-271 and
 :345-371) and launch asynchronously on torch's current stream.  The launch
 parameters block_m/block_n/num_warps/num_stages are accepted for
-compatibility; the gfx950 kernel uses its own fixed tile (256 queries x 64
-keys per workgroup for head_dim <= 128).  ``update_attention_state_int8``
+compatibility; the gfx950 kernel uses its own fixed tile (64 keys, and 384
+queries per workgroup for head_dim 72-128, 256 for head_dim <= 64).  ``update_attention_state_int8``
 (reference :274-342) dequantizes INT8 K/V inside the kernel.
 ``finalize_attention`` gains optional ``running_max`` / ``lse`` arguments
 that write the natural-log LSE ``[heads, tokens]``.

@@ -25,9 +25,9 @@ rows they are pinned to) are unchanged.
 
 gfx950 specifics: on a ROCm device the launch preset is (128, 64, 4, 2) for
 every head_dim: Q chunks align to 128 rows and K/V chunks to the kernel's
-64-key LDS tile (a workgroup covers 256 queries for head_dim <= 128, and
-the last workgroup of a chunk is masked, so 128-row alignment costs at most
-half a workgroup per chunk).  ``output_mode="host_aliased"`` charges no raw
+64-key LDS tile (a workgroup covers 384 queries for head_dim 72-128 and 256
+for head_dim <= 64, and the last workgroup of a chunk is masked, so 128-row
+alignment costs at most one partly masked workgroup per chunk).  ``output_mode="host_aliased"`` charges no raw
 output slots because the output is finalized into the Q buffer.
 """
 
