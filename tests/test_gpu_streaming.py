@@ -98,7 +98,10 @@ def test_matches_oracle_at_reference_test_shapes(dtype, causal, q_heads, kv_head
     check(out, lse, ref_o, ref_l)
 
 
-@pytest.mark.parametrize("head_dim", [16, 32, 48, 64, 96, 128, 200, 256])
+# Every kernel geometry and its edges: the 32-query kernel at head_dim 16-64
+# and 136-256, the 48-query kernel at 72-128, including head_dims that end
+# inside a 16-wide d block (40, 72, 104, 120) or a 32-wide d step (80).
+@pytest.mark.parametrize("head_dim", [16, 32, 40, 48, 64, 72, 80, 96, 104, 120, 128, 136, 200, 256])
 @pytest.mark.parametrize("causal", [False, True])
 def test_head_dims_ragged_chunks(head_dim, causal):
     announce(f"head_dim={head_dim} causal={causal}")
