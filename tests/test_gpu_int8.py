@@ -71,7 +71,9 @@ CASES = [
     (32, 4, 2, torch.float16, True),
     (48, 2, 1, torch.bfloat16, False),
     (64, 8, 2, torch.bfloat16, True),
+    (80, 4, 2, torch.bfloat16, True),
     (96, 2, 2, torch.float16, False),
+    (112, 6, 3, torch.float16, False),
     (128, 8, 4, torch.bfloat16, False),
     (128, 4, 4, torch.bfloat16, True),
 ]
