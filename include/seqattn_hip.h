@@ -24,7 +24,9 @@
 extern "C" {
 #endif
 
-#define SA_ABI_VERSION 1
+/* 2: pipeline state in 16-row groups (sa_pipeline_create); fused finalize in
+ * the pipeline's last chunk launches. */
+#define SA_ABI_VERSION 2
 
 /* dtype codes for Q/K/V/output element types */
 #define SA_DTYPE_BF16 0
@@ -163,12 +165,14 @@ typedef struct sa_pipeline_stats {
  *   k_slots[i], v_slots[i]  [kv_chunk_tokens, kv_heads, head_dim] dtype, i < num_kv_buffers (1..3)
  *   running_max, running_sum  q_rows * q_heads fp32
  *   accumulator   q_rows * q_heads * head_dim fp32
- *                 with q_rows = q_chunk_tokens rounded up to a multiple of 32.
+ *                 with q_rows = q_chunk_tokens rounded up to a multiple of 16.
  *                 The pipeline keeps this state in the update kernel's
- *                 row-group layout (32-row groups in lane order, so every
+ *                 row-group layout (16-row groups in lane order, so every
  *                 state load and store moves whole contiguous blocks), not in
  *                 the strided [token][head] layout of sa_update_attention_state;
- *                 only this pipeline's launches read it.
+ *                 only this pipeline's launches read it.  Buffers sized for
+ *                 q_chunk_tokens rows only are too small whenever
+ *                 q_chunk_tokens is not a multiple of 16 and q_heads > 1.
  *   out_slots     NULL (device-consumer mode: no raw output buffers) or
  *                 num_output_buffers pointers to [q_chunk_tokens, q_heads, head_dim] dtype
  *   num_output_buffers  1..2: output ready/free event pairs (and slots when out_slots != NULL)

@@ -137,11 +137,14 @@ struct UpdateParams {
   // stores l and the next one reloads it, so the result equals the chunked
   // schedule's bit for bit.
   int32_t merge_tiles = 0;
-  // Fused finalize, for launches that start the state and cover every key of
-  // their rows: when out is non-null the epilogue writes acc / l (0 where
-  // l == 0) to out and, when lse is non-null, (m + log2 l) ln 2 (-inf where
-  // l == 0) to lse[head * lse_sh + lse_off + query], with the expressions of
-  // finalize_kernel, and stores no state.
+  // Fused finalize, for the launch that applies the last keys of its rows
+  // (with or without loading the state first): when out is non-null the
+  // epilogue writes acc / l (0 where l == 0) to out and, when lse is
+  // non-null, (m + log2 l) ln 2 (-inf where l == 0) to
+  // lse[head * lse_sh + lse_off + query], with the expressions of
+  // finalize_kernel, and stores no state.  out may alias q: each query's
+  // row of one head is read (at the start) and written (at the end) by the
+  // same wave only.
   uint16_t* out = nullptr;
   int64_t so_t = 0, so_h = 0;
   float* lse = nullptr;
@@ -818,47 +821,6 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
   const uint16_t* kp = p.k + (int64_t)kv_head * p.sk_h;
   const uint16_t* vp = p.v + (int64_t)kv_head * p.sv_h;
 
-  // Q fragments: query qw0 + 16 qb + r16, d = 32 c + 8 j .. +7.
-  u32x4 qf[QB][4];
-  int qi[QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    qi[qb] = qw0 + 16 * qb + r16;
-    const bool ok = qi[qb] < p.q_tokens;
-#pragma unroll
-    for (int c = 0; c < 4; ++c) {
-      const int d = 32 * c + 8 * j;
-      if (ok && d < p.head_dim)
-        qf[qb][c] = *reinterpret_cast<const u32x4*>(qp + (int64_t)qi[qb] * p.sq_t + d) ^ q_sign(p.scale_log2);
-      else
-        qf[qb][c] = u32x4{0, 0, 0, 0};
-    }
-  }
-
-  // Online-softmax state; acc[db][qb] holds d = 16 db + 4 j .. +3 of query qi[qb].
-  float m_run[QB], l_part[QB];
-  f32x4 acc[8][QB];
-#pragma unroll
-  for (int qb = 0; qb < QB; ++qb) {
-    m_run[qb] = -INFINITY;
-    l_part[qb] = 0.f;
-#pragma unroll
-    for (int db = 0; db < 8; ++db) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    if (!INIT && qi[qb] < p.q_tokens) {
-      const int64_t blk = state_block(qi[qb], head, p.q_heads);
-      const int64_t srow = p.tiled_state ? blk * 16 + r16 : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
-      m_run[qb] = p.m[srow];
-      l_part[qb] = j == 0 ? p.l[srow] : 0.f;
-      const float* arow = p.tiled_state ? p.acc + blk * 16 * p.head_dim + 4 * lane
-                                        : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h + 4 * j;
-#pragma unroll
-      for (int db = 0; db < 8; ++db) {
-        if (16 * db + 4 * j < p.head_dim)
-          acc[db][qb] = *reinterpret_cast<const f32x4*>(arow + (p.tiled_state ? 256 * db : 16 * db));
-      }
-    }
-  }
-
   int kv_end = p.kv_tokens;
   if (CAUSAL) {
     const int q_last = min(p.q_tokens, q_block + Geo::BLOCK_M) - 1;
@@ -928,6 +890,54 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
       __builtin_amdgcn_global_load_lds((const SA_GLOBAL void*)(vb + vo), (SA_LDS void*)(v_stage + f * 1024), 16, 0, 0);
     }
   };
+
+  // The first tile's DMA is issued before the Q and state loads, so that it
+  // is in flight while they arrive (the 16-bit path; the INT8 path stages
+  // its own first tile).
+  if constexpr (!QUANT) {
+    if (ntiles > 0) issue_tile(0, lds_a);
+  }
+
+  // Q fragments: query qw0 + 16 qb + r16, d = 32 c + 8 j .. +7.
+  u32x4 qf[QB][4];
+  int qi[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    qi[qb] = qw0 + 16 * qb + r16;
+    const bool ok = qi[qb] < p.q_tokens;
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const int d = 32 * c + 8 * j;
+      if (ok && d < p.head_dim)
+        qf[qb][c] = *reinterpret_cast<const u32x4*>(qp + (int64_t)qi[qb] * p.sq_t + d) ^ q_sign(p.scale_log2);
+      else
+        qf[qb][c] = u32x4{0, 0, 0, 0};
+    }
+  }
+
+  // Online-softmax state; acc[db][qb] holds d = 16 db + 4 j .. +3 of query qi[qb].
+  float m_run[QB], l_part[QB];
+  f32x4 acc[8][QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = -INFINITY;
+    l_part[qb] = 0.f;
+#pragma unroll
+    for (int db = 0; db < 8; ++db) acc[db][qb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (!INIT && qi[qb] < p.q_tokens) {
+      const int64_t blk = state_block(qi[qb], head, p.q_heads);
+      const int64_t srow = p.tiled_state ? blk * 16 + r16 : (int64_t)qi[qb] * p.ss_t + (int64_t)head * p.ss_h;
+      m_run[qb] = p.m[srow];
+      l_part[qb] = j == 0 ? p.l[srow] : 0.f;
+      const float* arow = p.tiled_state ? p.acc + blk * 16 * p.head_dim + 4 * lane
+                                        : p.acc + (int64_t)qi[qb] * p.sa_t + (int64_t)head * p.sa_h + 4 * j;
+#pragma unroll
+      for (int db = 0; db < 8; ++db) {
+        if (16 * db + 4 * j < p.head_dim)
+          acc[db][qb] = *reinterpret_cast<const f32x4*>(arow + (p.tiled_state ? 256 * db : 16 * db));
+      }
+    }
+  }
 
   // Per-lane parts of the fragment addresses: 16 bytes per lane for the K and
   // V^T fragments, 8 bytes per lane for the transposing V reads.
@@ -1117,7 +1127,6 @@ __global__ __launch_bounds__(Geometry48::THREADS) void update48_kernel(const Upd
         }
       }
     };
-    if (ntiles > 0) issue_tile(0, lds_a);
     for (int t = 0; t < ntiles; t += 2) {
       tile(t, lds_a, lds_b);
       if (t + 1 < ntiles) tile(t + 1, lds_b, lds_a);
@@ -1275,48 +1284,54 @@ struct FinalizeParams {
   uint16_t* out;
   float* lse;
   int64_t sa_t, sa_h, ss_t, ss_h, so_t, so_h, lse_sh, lse_off;
-  int64_t total;  // q_tokens * q_heads * (head_dim / 8)
-  int32_t q_heads, groups;
+  int32_t q_tokens, q_heads, groups;  // groups = head_dim / 8
   int32_t tiled_state;  // state in the row-group layout (state_block)
 };
 
+// One workgroup per (16-row group, head): blockIdx.x is the row group and
+// blockIdx.y the head, so no thread divides 64-bit indices.  Item i of the
+// group covers row r = i % 16 and output granule g = i / 16 (d = 8g .. 8g +
+// 7).  In the row-group layout a wave's 64 items read 2 KB of consecutive
+// accumulator bytes (chunks 2g and 2g + 1 of 16 rows) and write 16 rows x 64
+// bytes of output.
 template <typename Op>
 __global__ __launch_bounds__(256) void finalize_kernel(const FinalizeParams p) {
-  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (idx >= p.total) return;
-  const int g = (int)(idx % p.groups);
-  const int64_t row = idx / p.groups;
-  const int h = (int)(row % p.q_heads);
-  const int64_t t = row / p.q_heads;
-  const int64_t blk = state_block(t, h, p.q_heads);
-  const int r = (int)(t & 15);
-  const int64_t srow = p.tiled_state ? blk * 16 + r : t * p.ss_t + h * p.ss_h;
-  const float l = p.l[srow];
-  f32x4 a0, a1;
-  if (p.tiled_state) {
-    // Chunks 2g and 2g + 1 (d = 8g .. 8g + 7) of row r.
-    const float* a = p.acc + blk * 16 * (p.groups * 8) + (2 * g * 16 + r) * 4;
-    a0 = *reinterpret_cast<const f32x4*>(a);
-    a1 = *reinterpret_cast<const f32x4*>(a + 16 * 4);
-  } else {
-    const float* a = p.acc + t * p.sa_t + h * p.sa_h + 8 * g;
-    a0 = *reinterpret_cast<const f32x4*>(a);
-    a1 = *reinterpret_cast<const f32x4*>(a + 4);
-  }
-  u32x4 o;
-  if (l > 0.f) {
-    o[0] = Op::pack2(a0[0] / l, a0[1] / l);
-    o[1] = Op::pack2(a0[2] / l, a0[3] / l);
-    o[2] = Op::pack2(a1[0] / l, a1[1] / l);
-    o[3] = Op::pack2(a1[2] / l, a1[3] / l);
-  } else {
-    o = u32x4{0, 0, 0, 0};
-  }
-  *reinterpret_cast<u32x4*>(p.out + t * p.so_t + h * p.so_h + 8 * g) = o;
-  if (p.lse != nullptr && g == 0) {
-    const float m = p.m[srow];
-    p.lse[h * p.lse_sh + p.lse_off + t] =
-        l > 0.f ? (m + log2f(l)) * 0.69314718055994530942f : -INFINITY;
+  const int h = blockIdx.y;
+  const int64_t row0 = (int64_t)blockIdx.x * 16;
+  const int64_t blk = state_block(row0, h, p.q_heads);
+  const int items = 16 * p.groups;
+  for (int i = threadIdx.x; i < items; i += 256) {
+    const int r = i & 15;
+    const int g = i >> 4;
+    const int64_t t = row0 + r;
+    if (t >= p.q_tokens) continue;
+    const int64_t srow = p.tiled_state ? blk * 16 + r : t * p.ss_t + h * p.ss_h;
+    const float l = p.l[srow];
+    f32x4 a0, a1;
+    if (p.tiled_state) {
+      // Chunks 2g and 2g + 1 (d = 8g .. 8g + 7) of row r.
+      const float* a = p.acc + blk * 16 * (p.groups * 8) + (2 * g * 16 + r) * 4;
+      a0 = *reinterpret_cast<const f32x4*>(a);
+      a1 = *reinterpret_cast<const f32x4*>(a + 16 * 4);
+    } else {
+      const float* a = p.acc + t * p.sa_t + h * p.sa_h + 8 * g;
+      a0 = *reinterpret_cast<const f32x4*>(a);
+      a1 = *reinterpret_cast<const f32x4*>(a + 4);
+    }
+    u32x4 o;
+    if (l > 0.f) {
+      o[0] = Op::pack2(a0[0] / l, a0[1] / l);
+      o[1] = Op::pack2(a0[2] / l, a0[3] / l);
+      o[2] = Op::pack2(a1[0] / l, a1[1] / l);
+      o[3] = Op::pack2(a1[2] / l, a1[3] / l);
+    } else {
+      o = u32x4{0, 0, 0, 0};
+    }
+    *reinterpret_cast<u32x4*>(p.out + t * p.so_t + h * p.so_h + 8 * g) = o;
+    if (p.lse != nullptr && g == 0) {
+      const float m = p.m[srow];
+      p.lse[h * p.lse_sh + p.lse_off + t] = l > 0.f ? (m + log2f(l)) * 0.69314718055994530942f : -INFINITY;
+    }
   }
 }
 
@@ -1485,9 +1500,10 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
     return SA_ERR_INVALID_ARGUMENT;
   }
   if (q_tokens == 0) return 0;
-  // A fused launch initializes its state and writes the output instead of
-  // the state: m, l and acc are not touched and may be null.
-  if (!q || !k || !v || (fused == nullptr && (!m || !l || !acc))) {
+  // A fused launch writes the output instead of the state; one that also
+  // initializes the state does not touch m, l and acc, which may be null.
+  const bool starts_state = (flags & SA_FLAG_INITIALIZE) != 0;
+  if (!q || !k || !v || (!(fused != nullptr && starts_state) && (!m || !l || !acc))) {
     set_error("sa_update_attention_state: null pointer argument");
     return SA_ERR_INVALID_ARGUMENT;
   }
@@ -1534,10 +1550,8 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
   p.tiled_state = tiled_state ? 1 : 0;
   if (fused != nullptr) {
     // Same output layout rules as the finalize kernel.
-    if (!(flags & SA_FLAG_INITIALIZE) || !fused->out || fused->so_t % 8 != 0 || fused->so_h % 8 != 0 ||
-        !aligned(fused->out, 16)) {
-      set_error("fused finalize needs an initializing launch and a 16-byte aligned output with "
-                "vector-aligned strides");
+    if (!fused->out || fused->so_t % 8 != 0 || fused->so_h % 8 != 0 || !aligned(fused->out, 16)) {
+      set_error("fused finalize needs a 16-byte aligned output with vector-aligned strides");
       return SA_ERR_INVALID_ARGUMENT;
     }
     p.out = static_cast<uint16_t*>(fused->out);
@@ -1718,10 +1732,14 @@ int32_t launch_finalize(const float* acc, const float* m, const float* l, void* 
   p.lse_sh = lse_sh;
   p.lse_off = lse_off;
   p.groups = head_dim / 8;
+  p.q_tokens = q_tokens;
   p.q_heads = q_heads;
   p.tiled_state = tiled_state ? 1 : 0;
-  p.total = (int64_t)q_tokens * q_heads * p.groups;
-  const dim3 grid((unsigned)((p.total + 255) / 256));
+  if (q_heads > 65535) {
+    set_error("sa_finalize_attention: q_heads %d exceeds the grid's 65,535 heads", q_heads);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  const dim3 grid((unsigned)(((int64_t)q_tokens + 15) / 16), (unsigned)q_heads);
   if (dtype == SA_DTYPE_BF16)
     hipLaunchKernelGGL(finalize_kernel<BF16>, grid, dim3(256), 0, stream, p);
   else
@@ -1805,6 +1823,21 @@ int32_t sa_run_resident_noalloc(const void* q, const void* k, const void* v, voi
     sa::set_error("sa_run_resident_noalloc: out must be 16-byte aligned with strides that are multiples of 8");
     return SA_ERR_INVALID_ARGUMENT;
   }
+  // The launches' own argument rules, checked here so that a call they would
+  // reject is rejected before anything is enqueued on the shared scratch.
+  const int64_t in_strides[] = {stride_qt, stride_qh, stride_kt, stride_kh, stride_vt, stride_vh};
+  for (int64_t st : in_strides) {
+    if (st % 8 != 0) {
+      sa::set_error("sa_run_resident_noalloc: q/k/v token and head strides must be multiples of 8 elements");
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+  }
+  if (stride_kt <= 0 || stride_kt >= (1 << 24) || !aligned(q, 16) || !aligned(k, 16) || !aligned(v, 16) ||
+      (lse != nullptr && !aligned(lse, 4))) {
+    sa::set_error("sa_run_resident_noalloc: q/k/v must be 16-byte aligned (lse 4-byte) and the k token stride "
+                  "in [1, 2^24) elements");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
   // Every segment is checked before anything is enqueued.
   for (int32_t s = 0; s < num_segments; ++s) {
     const int64_t q_length = cu_seqlens_q[s + 1] - cu_seqlens_q[s];
@@ -1812,6 +1845,11 @@ int32_t sa_run_resident_noalloc(const void* q, const void* k, const void* v, voi
     if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0) || q_length > INT32_MAX ||
         k_length >= (1 << 24)) {
       sa::set_error("sa_run_resident_noalloc: segment %d has invalid bounds", s);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    // Workgroup numbering of the update launch is 32-bit.
+    if ((q_length + 127) / 128 * q_heads > (int64_t)INT32_MAX / 8) {
+      sa::set_error("sa_run_resident_noalloc: segment %d has too many queries x heads for one launch", s);
       return SA_ERR_INVALID_ARGUMENT;
     }
     const int64_t needed = (int64_t)kv_heads * 128 * ((k_length + 63) / 64 * 64) * 2;

@@ -329,12 +329,17 @@ struct SideJoin {
 // change nothing and are neither copied nor launched, except that a chunk
 // always runs while the state is uninitialized.  `after_copy`, if given, is
 // called with the chunk's ordinal once its H2D copies are enqueued, so the
-// caller can slot other H2D work between chunks.
+// caller can slot other H2D work between chunks.  `fused_last`, if given,
+// describes the output (and LSE) of row 0 of the block: the span's last
+// launch then writes acc / l and the LSE in its epilogue instead of storing
+// the state, with the finalize kernel's expressions, and *fused_done is set.
+// The caller runs the finalize kernel itself when no launch was made.
 int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, const KVSource& src,
                    int32_t kv_tokens, int32_t kv_local_offset, bool* initialize,
                    int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
                    int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
-                   const std::function<int32_t(int32_t)>* after_copy = nullptr) {
+                   const std::function<int32_t(int32_t)>* after_copy = nullptr,
+                   const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr) {
   if (kv_tokens < 0 || kv_local_offset < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad K/V span kv_tokens=%d kv_local_offset=%d q_tokens=%d", kv_tokens,
                   kv_local_offset, q_tokens);
@@ -349,6 +354,23 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
   const int32_t split = (!src.on_device && q_tokens >= 2 * tile) ? (q_tokens / 2 + tile - 1) / tile * tile : q_tokens;
   const bool two = split < q_tokens && kv_tokens > 0;
   const char* q_second = static_cast<const char*>(q) + (int64_t)split * sq_t * 2;
+  // Start of the last chunk the loop below launches (-1: none).
+  int64_t last_start = -1;
+  {
+    bool init = *initialize;
+    for (int32_t start = 0; start < kv_tokens; start += p->kv_chunk) {
+      if (!init && (int64_t)kv_local_offset + start >= visible_end) break;
+      last_start = start;
+      init = false;
+    }
+  }
+  sa::FusedOutput out_first{}, out_second{};
+  if (fused_last != nullptr) {
+    out_first = *fused_last;
+    out_second = *fused_last;
+    out_second.out = static_cast<char*>(fused_last->out) + (int64_t)split * fused_last->so_t * 2;
+    out_second.lse_off = fused_last->lse_off + split;
+  }
   SideJoin join{p, compute};
   if (two) {
     SA_HIP_RETURN(hipEventRecord(p->fork, compute));
@@ -360,11 +382,14 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
     if (!*initialize && position >= visible_end) break;
     const int32_t n = std::min(p->kv_chunk, kv_tokens - start);
     const int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (*initialize ? SA_FLAG_INITIALIZE : 0);
+    const bool fuse = fused_last != nullptr && start == last_start;
+    if (fuse && fused_done) *fused_done = true;
     int32_t rc;
     if (src.on_device) {
       rc = launch_timed(p, q, sq_t, sq_h, src.k + start * src.sk_t * 2, src.sk_t, src.sk_h,
                         src.v + start * src.sv_t * 2, src.sv_t, src.sv_h, q_tokens, n,
-                        q_local_offset, (int32_t)position, causal_shift, scale, flags, compute);
+                        q_local_offset, (int32_t)position, causal_shift, scale, flags, compute, 0,
+                        fuse ? &out_first : nullptr);
       if (rc != 0) return rc;
       add_stats(st, 0, 0, 0, 1, 0);
     } else {
@@ -388,7 +413,7 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
       SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
       rc = launch_timed(p, q, sq_t, sq_h, p->k_slots[slot], kt, p->head_dim, p->v_slots[slot], kt,
                         p->head_dim, split, n, q_local_offset, (int32_t)position, causal_shift,
-                        scale, flags, compute);
+                        scale, flags, compute, 0, fuse ? &out_first : nullptr);
       if (rc != 0) return rc;
       SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
       p->kv_pending[slot] = true;
@@ -396,7 +421,7 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
         SA_HIP_RETURN(hipStreamWaitEvent(p->side, p->kv_ready[slot], 0));
         rc = launch_timed(p, q_second, sq_t, sq_h, p->k_slots[slot], kt, p->head_dim, p->v_slots[slot], kt,
                           p->head_dim, q_tokens - split, n, q_local_offset + split, (int32_t)position,
-                          causal_shift, scale, flags, p->side, 0, nullptr, split);
+                          causal_shift, scale, flags, p->side, 0, fuse ? &out_second : nullptr, split);
         if (rc != 0) return rc;
         SA_HIP_RETURN(hipEventRecord(p->kv_free_side[slot], p->side));
         p->kv_side_pending[slot] = true;
@@ -523,7 +548,8 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
                   int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
                   int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
                   const void* q_block = nullptr,
-                  const std::function<int32_t(int32_t)>* after_copy = nullptr) {
+                  const std::function<int32_t(int32_t)>* after_copy = nullptr,
+                  const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr) {
   if (k_length < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad stream_kv sizes k_length=%d q_tokens=%d", k_length, q_tokens);
     return SA_ERR_INVALID_ARGUMENT;
@@ -533,7 +559,7 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
   KVSource src{static_cast<const char*>(k_host), static_cast<const char*>(v_host), false, 0, 0, 0, 0};
   bool initialize = true;
   int32_t rc = apply_span(p, q, qt, p->head_dim, src, k_length, 0, &initialize, q_tokens, q_local_offset,
-                          causal_shift, scale, causal, compute, st, after_copy);
+                          causal_shift, scale, causal, compute, st, after_copy, fused_last, fused_done);
   if (rc != 0) return rc;
   if (initialize)
     return init_state(p, q, qt, p->head_dim, q_tokens, q_local_offset, causal_shift, scale, compute);
@@ -672,17 +698,25 @@ int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const ch
       return 0;
     };
     SA_HIP_RETURN(hipStreamWaitEvent(compute, p->alt_ready[b], 0));
+    // The pass's last chunk launches write the output into the pass's own Q
+    // buffer (each query row is read and written by one wave only) and the
+    // LSE, in place of a state store and a finalize launch.
+    const sa::FusedOutput fused{buf[b], q_stride, p->head_dim, lse, lse_sh, ps.qt};
+    bool fused_done = false;
     rc = stream_kv(p, kh + ps.k_start * p->kv_row_bytes, vh + ps.k_start * p->kv_row_bytes, ps.k_len, ps.n,
-                   ps.q_local, ps.causal_shift, scale, causal, compute, st, buf[b], &between_chunks);
+                   ps.q_local, ps.causal_shift, scale, causal, compute, st, buf[b], &between_chunks, &fused,
+                   &fused_done);
     if (rc) return rc;
     while (has_next && next_piece < kPieces)
       if ((rc = copy_piece(i + 1, next_piece++)) != 0) return rc;
     {
       TraceRange range(p->trace, "seqattn:fused_finalize");
-      rc = sa::launch_finalize(p->acc, p->m, p->l, buf[b], lse, q_stride, p->head_dim, p->q_heads, 1, q_stride,
-                               p->head_dim, lse_sh, ps.qt, ps.n, p->q_heads, p->head_dim, p->dtype, compute,
-                               /*tiled_state=*/true);
-      if (rc) return rc;
+      if (!fused_done) {
+        rc = sa::launch_finalize(p->acc, p->m, p->l, buf[b], lse, q_stride, p->head_dim, p->q_heads, 1, q_stride,
+                                 p->head_dim, lse_sh, ps.qt, ps.n, p->q_heads, p->head_dim, p->dtype, compute,
+                                 /*tiled_state=*/true);
+        if (rc) return rc;
+      }
       SA_HIP_RETURN(hipEventRecord(p->alt_done[b], compute));
     }
     const int64_t bytes = (int64_t)ps.n * p->q_row_bytes;
@@ -1264,9 +1298,15 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
       const int32_t n = (int32_t)std::min<int64_t>(block, q_stop - qt);
       int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
       if (rc) return rc;
+      // Without output slots the block is finalized into the Q buffer, which
+      // the last chunk launches do themselves in their epilogue.
+      const int64_t q_stride = (int64_t)p->q_heads * p->head_dim;
+      const sa::FusedOutput fused{p->q_buffer, q_stride, p->head_dim, lse, lse_stride_h, qt};
+      bool fused_done = false;
       rc = stream_kv(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
                      (int32_t)k_length, n, (int32_t)(qt - q_start), causal_shift, softmax_scale,
-                     causal, compute, stats);
+                     causal, compute, stats, nullptr, nullptr, p->has_out_slots ? nullptr : &fused,
+                     &fused_done);
       if (rc) return rc;
       const int32_t slot = (int32_t)(chunk_index % p->num_out);
       const int64_t bytes = (int64_t)n * p->q_row_bytes;
@@ -1275,8 +1315,10 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
         if (rc) return rc;
         rc = d2h(p, oh + qt * p->q_row_bytes, p->out_slots[slot], bytes, slot, 0, compute, stats);
       } else {
-        rc = finalize(p, -1, n, lse, lse_stride_h, qt, compute);
-        if (rc) return rc;
+        if (!fused_done) {
+          rc = finalize(p, -1, n, lse, lse_stride_h, qt, compute);
+          if (rc) return rc;
+        }
         rc = d2h(p, oh + qt * p->q_row_bytes, p->q_buffer, bytes, slot, 1, compute, stats);
       }
       if (rc) return rc;

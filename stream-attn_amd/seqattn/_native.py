@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libseqattn_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 SA_DTYPE_BF16 = 0
 SA_DTYPE_FP16 = 1

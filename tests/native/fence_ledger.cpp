@@ -175,13 +175,18 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
   op.reads.push_back(rows_of(q, q_tokens, sq_t, 2));
   op.reads.push_back(rows_of(k, kv_tokens, sk_t, 2));
   op.reads.push_back(v_transposed ? span(v, kv_heads * sv_h * 2) : rows_of(v, kv_tokens, sv_t, 2));
+  // A state-loading launch reads m, l and acc; a fused one writes the output
+  // and the LSE (it may alias q) instead of storing the state.
+  std::vector<Range> state;
+  if (!fused || !(flags & SA_FLAG_INITIALIZE)) {
+    const int64_t rows = state_rows(q_tokens, tiled);
+    state = {rows_of(m, rows, ss_t, 4), rows_of(l, rows, ss_t, 4), rows_of(acc, rows, sa_t, 4)};
+  }
+  if (!(flags & SA_FLAG_INITIALIZE)) op.reads.insert(op.reads.end(), state.begin(), state.end());
   if (fused) {
     op.writes.push_back(rows_of(fused->out, q_tokens, fused->so_t, 2));
     lse_ranges(op.writes, fused->lse, fused->lse_sh, fused->lse_off, q_tokens, q_heads);
   } else {
-    const int64_t rows = state_rows(q_tokens, tiled);
-    std::vector<Range> state = {rows_of(m, rows, ss_t, 4), rows_of(l, rows, ss_t, 4), rows_of(acc, rows, sa_t, 4)};
-    if (!(flags & SA_FLAG_INITIALIZE)) op.reads.insert(op.reads.end(), state.begin(), state.end());
     op.writes = state;
   }
   push(std::move(op));

@@ -101,10 +101,12 @@ def test_noalloc_entry_point_rejects_bad_arguments_before_touching_the_gpu():
     lib = _native.lib()
     fake = 1 << 40  # never dereferenced: every case below is rejected by the host-side checks
 
-    def call(cu_q, cu_k, *, heads=(8, 2), head_dim=128, dtype=0, kv_chunk=8192, q=fake):
+    def call(cu_q, cu_k, *, heads=(8, 2), head_dim=128, dtype=0, kv_chunk=8192, q=fake, k=fake, lse=None,
+             strides=None):
         qa = (ctypes.c_int64 * len(cu_q))(*cu_q)
         ka = (ctypes.c_int64 * len(cu_k))(*cu_k)
-        return lib.sa_run_resident_noalloc(q, fake, fake, fake, None, *([8 * 128] * 9), qa, ka, len(cu_q) - 1,
+        strides = strides if strides is not None else [8 * 128] * 9
+        return lib.sa_run_resident_noalloc(q, k, fake, fake, lse, *strides, qa, ka, len(cu_q) - 1,
                                            heads[0], heads[1], head_dim, dtype, kv_chunk, 0.1, 0, None)
 
     assert call([0, 10], [0, 10], head_dim=64) == -3 and b"head_dim 128" in lib.sa_last_error()
@@ -112,6 +114,18 @@ def test_noalloc_entry_point_rejects_bad_arguments_before_touching_the_gpu():
     assert call([0, 10], [0, 10], kv_chunk=100) == -1 and b"multiple of 64" in lib.sa_last_error()
     assert call([0, 10], [0, 10], q=None) == -1 and b"null" in lib.sa_last_error()
     assert call([0, 10], [0, 0]) == -1 and b"invalid bounds" in lib.sa_last_error()
+    # Stride, alignment and launch-size rules of the update and transpose
+    # launches are checked before the first launch is enqueued.
+    for i in range(6):  # q, k, v token/head strides
+        bad = [8 * 128] * 9
+        bad[i] = 8 * 128 + 4
+        assert call([0, 10], [0, 10], strides=bad) == -1 and b"multiples of 8" in lib.sa_last_error()
+    bad = [8 * 128] * 9
+    bad[2] = 1 << 24  # k token stride
+    assert call([0, 10], [0, 10], strides=bad) == -1 and b"2^24" in lib.sa_last_error()
+    assert call([0, 10], [0, 10], k=fake + 8) == -1 and b"16-byte aligned" in lib.sa_last_error()
+    assert call([0, 10], [0, 10], lse=fake + 2) == -1 and b"16-byte aligned" in lib.sa_last_error()
+    assert call([0, 1 << 30], [0, 64], heads=(64, 2)) == -1 and b"too many queries" in lib.sa_last_error()
     # 2 K/V heads x 128 x 131,072 keys x 2 bytes = 64 MiB fits; one more tile does not.
     assert call([0, 1, 2], [0, 131_072, 131_072 + 131_073]) == -1
     message = lib.sa_last_error()
