@@ -16,6 +16,12 @@ from concurrent.futures import ThreadPoolExecutor
 import numpy as np
 import torch
 
+class RunModeNotice(UserWarning):
+    """Names the mode a GPU configuration test ran in (for example whether a
+    store was read with O_DIRECT), so that the mode shows in pytest's
+    warnings summary even under -q."""
+
+
 O_TOL = 2e-2
 LSE_TOL = 1e-3
 REL_L2_TOL = 5e-3

@@ -3,7 +3,8 @@
 Each case runs the product path (libseqattn_hip.so through the seqattn API)
 on the configuration's own shape and seeded inputs and compares the output
 and the natural-log LSE with the CPU oracle: all rows for the 4,096-token
-case, and for the long sequences the reference's large-tier signature rows
+case, and for the long sequences (the 524,288-token workspace sweep is in
+test_gpu_config3_sweep.py) the reference's large-tier signature rows
 {0, N/4, N/2, 3N/4, N-1} (benchmarks/large_tier_comparison.py:62-66) plus
 1,024 seeded-random rows, every head, against every key.  Tolerances: O
 max-abs <= 2e-2, LSE max-abs <= 1e-3, O relative L2 <= 5e-3, every element
@@ -14,6 +15,7 @@ from __future__ import annotations
 
 import os
 import tempfile
+import warnings
 from pathlib import Path
 
 import numpy as np
@@ -35,6 +37,7 @@ from seqattn import (
     streaming_attn_varlen_func,
 )
 from seeded import (
+    RunModeNotice,
     check_parity,
     oracle_rows,
     release_host_memory,
@@ -82,34 +85,6 @@ def test_config1_4096x8x64_all_rows_on_the_hip_path():
 
 
 @pytest.mark.timeout(900)
-def test_config3_524k_56h_pinned_dram_2gib_workspace():
-    n, h, d = 524_288, 56, 128
-    announce(f"config 3: {n} x {h} x {d} bf16, pinned DRAM -> pinned DRAM, 2 GiB workspace")
-    q, k, v = seeded_qkv(n, h, d, seed=0)
-    cu = torch.tensor([0, n], dtype=torch.int32)
-    config = StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30, backend="hip")
-    plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
-                      max_q_tokens=n, max_kv_tokens=n, config=config)
-    # The reference planner's choice at 2 GiB (README.md:62).
-    assert (plan.q_chunk_tokens, plan.kv_chunk_tokens, plan.q_passes) == (28_416, 8_192, 19)
-    runner = StreamingAttentionRunner(plan, config)
-    out = torch.empty((n, h, d), dtype=torch.bfloat16, pin_memory=True)
-    lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
-    stats = StreamingAttentionStats()
-    runner(q, k, v, cu, cu, out=out, lse_out=lse, stats=stats)
-    torch.cuda.synchronize()
-    runner.close()
-    print(f"    step done: {stats.wall_seconds:.2f} s, H2D {stats.h2d_bytes / 1e9:.1f} GB", flush=True)
-    assert stats.h2d_bytes == n * h * d * 2 * (1 + 2 * plan.q_passes)
-    assert stats.d2h_bytes == n * h * d * 2
-    rows = signature_and_random_rows(n, 1024, seed=3)
-    ref_o, ref_l = oracle_rows(q, k, v, rows, kv_chunk=plan.kv_chunk_tokens)
-    idx = torch.from_numpy(rows)
-    check_parity(out[idx].float().numpy(), lse[:, idx.cuda()].cpu().numpy(), ref_o, ref_l,
-                 f"{rows.size} rows x {h} heads")
-
-
-@pytest.mark.timeout(900)
 def test_config4_paged_158k_48h_256_token_pages_from_an_aligned_store():
     n, h, d, page_tokens = 158_208, 48, 128, 256
     announce(f"config 4: paged {n} x {h} x {d}, {page_tokens}-token pages, O_DIRECT store, 16 GiB cache")
@@ -124,8 +99,10 @@ def test_config4_paged_158k_48h_256_token_pages_from_an_aligned_store():
             store = NvmeQKVWriter.from_tensors(root / "qkv", q, k, v, cu, cu, page_target_bytes=page_bytes,
                                                block_n=64, direct_io=True)
             direct_io = True
-        except RuntimeError:
+            refused = ""
+        except RuntimeError as error:
             # A filesystem without O_DIRECT (tmpfs): the same records, buffered.
+            refused = f"{error}"
             store = NvmeQKVWriter.from_tensors(root / "qkv-buffered", q, k, v, cu, cu,
                                                page_target_bytes=page_bytes, block_n=64, direct_io=False)
             direct_io = False
@@ -143,6 +120,9 @@ def test_config4_paged_158k_48h_256_token_pages_from_an_aligned_store():
         stats = PagedAttentionStats()
         runner.run_with_device_output(store, store, cu, cu, out=out, lse_out=lse, stats=stats)
         torch.cuda.synchronize()
+    warnings.warn(RunModeNotice(
+        f"config 4 read its pages from an O_DIRECT store under {parent}" if direct_io else
+        f"config 4 read its pages from a BUFFERED store under {parent}: O_DIRECT was refused ({refused})"))
     print(f"    direct_io={direct_io} cache hit ratio {stats.cache_hit_ratio:.3f} "
           f"q chunks {stats.q_chunks} kv pages {stats.kv_pages}", flush=True)
     rows = signature_and_random_rows(n, 1024, seed=4)
@@ -167,8 +147,12 @@ def test_config5_1m_64h_peaked_keys_8gib_workspace():
     try:
         out = torch.empty((n, h, d), dtype=torch.bfloat16, pin_memory=True)
     except RuntimeError as error:
-        print(f"    page-locking the 16 GiB output failed ({type(error).__name__}); output is pageable", flush=True)
+        refused = f"{type(error).__name__}: {error}"
         out = torch.empty((n, h, d), dtype=torch.bfloat16)
+    warnings.warn(RunModeNotice(
+        "config 5 wrote its output to page-locked host memory" if out.is_pinned() else
+        f"config 5 wrote its output to PAGEABLE host memory (page-locking 16 GiB failed: {refused}); its copies "
+        "went through the runtime's staging"))
     config = StreamingAttentionConfig(workspace_budget_bytes=8 * 2**30, kv_chunk_tokens=8192, backend="hip",
                                       pin_output=out.is_pinned())
     plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",

@@ -226,3 +226,37 @@ def test_cpu_plumbing_4096_tokens_8_heads():
     ref_o, ref_l = dense_attention_f64(q, k, v, cu, cu, rows=rows)
     np.testing.assert_allclose(out[rows], ref_o[rows], atol=2e-5, rtol=2e-5)
     np.testing.assert_allclose(lse[:, rows], ref_l[:, rows], atol=2e-5)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("workers", [3, 4])
+def test_head_split_and_bf16_bit_pattern_paths_equal_the_single_threaded_float_path(causal, workers):
+    # The GPU configuration tests and the bench run the oracle on bf16 bit
+    # patterns (uint16 views of the pinned tensors) with the K/V heads split
+    # over threads.  Both must give exactly what one thread gives on the same
+    # values widened to float32: 8 query heads over 4 K/V heads (GQA), ragged
+    # segments, 3 workers (uneven head groups) and 4.
+    from threadpoolctl import threadpool_limits
+
+    gen = torch.Generator().manual_seed(5)
+    q = torch.randn(300, 8, 64, generator=gen).to(torch.bfloat16)
+    k = torch.randn(350, 4, 64, generator=gen).to(torch.bfloat16)
+    v = torch.randn(350, 4, 64, generator=gen).to(torch.bfloat16)
+    cu_q, cu_k = bounds([100, 200]), bounds([150, 200])
+
+    def bits(t):
+        return t.view(torch.int16).numpy().view(np.uint16)
+
+    with threadpool_limits(1):
+        ref_o, ref_l = chunked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu_q, cu_k,
+                                         q_chunk_tokens=64, kv_chunk_tokens=48, causal=causal, workers=1)
+        got_o, got_l = chunked_attention(bits(q), bits(k), bits(v), cu_q, cu_k, q_chunk_tokens=64,
+                                         kv_chunk_tokens=48, causal=causal, workers=workers)
+    assert np.isfinite(ref_o).all()
+    assert np.array_equal(got_o, ref_o)
+    assert np.array_equal(got_l, ref_l)
+    # and the float path is itself pinned to the float64 closed form
+    dense_o, dense_l = dense_attention_f64(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu_q, cu_k,
+                                           causal=causal)
+    np.testing.assert_allclose(got_o, dense_o, atol=2e-5, rtol=2e-5)
+    np.testing.assert_allclose(got_l, dense_l, atol=2e-5, rtol=2e-5)
