@@ -10,7 +10,13 @@ native pipeline (streams, events), which costs more to build than a small
 attention call takes to run, so these functions keep the runner of the last
 (plan, config) pair and reuse it while calls repeat it.  A lock serializes
 calls on the shared runner, so concurrent callers stay correct.
-``clear_runner_cache()`` releases it; a different plan replaces it.
+
+Memory kept between calls: the cached runner's workspace, about the plan's
+``estimated_workspace_bytes`` of HBM (at most the config's
+``workspace_budget_bytes``), and its pipeline's streams and events.  The
+transposed-V scratch of an HBM-resident call (as large as V) is dropped when
+the call returns, and a call that raises drops the runner itself.
+``clear_runner_cache()`` releases the runner; a different plan replaces it.
 """
 
 from __future__ import annotations
@@ -46,7 +52,17 @@ def _run_cached(plan: AttentionPlan, config: StreamingAttentionConfig, call):
                 _cached[1].close()
                 _cached = None
             _cached = (key, StreamingAttentionRunner(plan, config))
-        return call(_cached[1])
+        runner = _cached[1]
+        try:
+            result = call(runner)
+        except BaseException:
+            # A call that raised may have left work of its own on the
+            # runner's buffers: drop the runner instead of reusing it.
+            _cached = None
+            runner.close()
+            raise
+        runner.release_resident_scratch()
+        return result
 
 
 def _longest_segment(cu_seqlens: torch.Tensor) -> int:

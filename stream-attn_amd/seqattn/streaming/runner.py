@@ -52,6 +52,12 @@ class StreamingAttentionRunner(HipExecutorMixin):
         if self._workspace is not None:
             self._workspace.close()
 
+    def release_resident_scratch(self) -> None:
+        """Drop the transposed-V scratch that HBM-resident runs keep for the
+        next run (as large as V; outside the planner's budget)."""
+        if self._workspace is not None:
+            self._workspace.release_resident_scratch()
+
     def _validate_inputs(
         self,
         q_cpu: torch.Tensor,

@@ -164,6 +164,15 @@ class CudaWorkspace:
         self.resident_scratch = scratch
         return needed
 
+    def release_resident_scratch(self) -> None:
+        """Detach and drop the transposed-V scratch.  Runs already enqueued
+        still read it: the buffer was allocated on the compute stream, so
+        the caching allocator hands its memory out again only to work
+        ordered after them."""
+        if self.resident_scratch is not None:
+            self._attach(None)
+            self.resident_scratch = None
+
     def close(self) -> None:
         handle = getattr(self, "handle", None)
         if handle is not None and handle.value:

@@ -39,3 +39,39 @@ def test_config_validation():
     PagedAttentionConfig().validate()
     with pytest.raises(ValueError, match="room for the DRAM cache"):
         PagedAttentionConfig(host_memory_budget_bytes=1 * 2**30).validate()
+
+
+def test_api_runner_cache_drops_a_runner_whose_call_raised_and_keeps_no_resident_scratch(monkeypatch):
+    # The FlashAttention-style wrappers keep the last runner; a stand-in
+    # runner (no GPU needed) records what the cache does with it.
+    import seqattn.api as api
+
+    events = []
+
+    class FakeRunner:
+        def __init__(self, plan, config):
+            self.id = len([e for e in events if e[0] == "new"])
+            events.append(("new", self.id))
+
+        def close(self):
+            events.append(("close", self.id))
+
+        def release_resident_scratch(self):
+            events.append(("release", self.id))
+
+    monkeypatch.setattr(api, "StreamingAttentionRunner", FakeRunner)
+    api.clear_runner_cache()
+    key = ("plan", "config")
+    assert api._run_cached(*key, lambda r: "ok") == "ok"
+    assert api._run_cached(*key, lambda r: "again") == "again"
+    assert events == [("new", 0), ("release", 0), ("release", 0)]
+
+    def boom(runner):
+        raise RuntimeError("kernel launch failed")
+
+    with pytest.raises(RuntimeError, match="kernel launch failed"):
+        api._run_cached(*key, boom)
+    assert events[-1] == ("close", 0) and api._cached is None
+    assert api._run_cached(*key, lambda r: r.id) == 1  # a fresh runner
+    api.clear_runner_cache()
+    assert events[-1] == ("close", 1) and api._cached is None
