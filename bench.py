@@ -21,7 +21,12 @@ two concurrent launches, one per half of the Q block's rows, on two streams.
   step over all queries and keys with the finalize fused (no PCIe);
 * cpu_baseline: the CPU oracle (numpy restatement of the reference's chunked
   FP32 attention) timed on this host on a bounded row sample, which is also
-  the parity check of the sampled rows (O and LSE) of both legs.
+  the parity check of the sampled rows (O and LSE) of both legs;
+* config2_65k and config4_paged: the benchmark's other configurations,
+  measured after the headline leg's buffers are released (65,536 tokens x
+  32 heads resident and streamed with 1 GiB; 158,208 tokens x 48 heads from
+  a 256-token page store), each with TFLOPS, MFMA-peak and PCIe fractions and
+  its own sampled-row parity.
 
 Effective TFLOPS = 4 * heads * head_dim * tokens^2 / seconds per step (the
 reference's definition, benchmarking/streaming.py:206).  Prints ONE JSON line.
@@ -50,6 +55,16 @@ PUBLISHED_TFLOPS = 217.4  # reference, same workload and budget (RTX 5090), READ
 
 def log(msg: str) -> None:
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def release_memory() -> None:
+    """Return freed device and page-locked host blocks (torch caches both)."""
+    import torch
+
+    gc.collect()
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    torch._C._host_emptyCache()
 
 
 def parse_args():
@@ -86,6 +101,11 @@ def parse_args():
                          "heads, peaked scores, 8 GiB workspace, with LSE; 65k: 65,536 tokens x 32 heads "
                          "resident in HBM and streamed with 1 GiB; projected: 61,312 tokens of hidden "
                          "size 5,376 through QKV projection, attention and output projection")
+    ap.add_argument("--side-workloads", default="65k,paged",
+                    help="streamed workload: other configurations measured after the headline leg and "
+                         "reported as keys of the same line (65k, paged; 'none' for neither)")
+    ap.add_argument("--side-steps", type=int, default=3, help="timed steps of each side workload")
+    ap.add_argument("--side-warmup", type=int, default=1, help="warmup steps of each side workload")
     ap.add_argument("--kv-storage", default="bf16", choices=["bf16", "int8"],
                     help="paged workload: K/V page storage dtype (int8: per-64-token-group scales, "
                          "dequantized in the kernel)")
@@ -483,21 +503,52 @@ def main() -> int:
         "cpu_baseline": cpu_baseline,
         "parity": parity,
     }
-    print(json.dumps(result), flush=True)
     # Release the pipeline, the device buffers and the page-locked host
-    # buffers before the interpreter shuts down.
+    # buffers before the side workloads (and before the interpreter shuts
+    # down).
     runner.close()
     del out_host, out_dev, lse_pinned, lse_res, q, k, v, runner
-    gc.collect()
-    torch.cuda.synchronize()
-    torch.cuda.empty_cache()
-    torch._C._host_emptyCache()
-    return 0 if (parity is None or parity["ok"]) else 1
+    release_memory()
+    side_ok = run_side_workloads(args, result, h2d_peak)
+    print(json.dumps(result), flush=True)
+    return 0 if (parity is None or parity["ok"]) and side_ok else 1
 
 
-def sampled_parity(q, k, v, out, lse, rows, kv_chunk, workers, scale=None):
-    """Oracle O (and LSE) on sampled query rows against the GPU result; also
-    the CPU baseline timing (returns parity dict, seconds)."""
+# Keys of a workload's own result line that a side entry leaves out (the
+# headline line carries them).
+_SIDE_DROP = ("n_gpus", "higher_is_better", "scaling", "vs_baseline", "dtype", "unit")
+
+
+def run_side_workloads(args, result, h2d_peak) -> bool:
+    """The other configurations of the benchmark, measured in the same
+    process after the headline leg, each with its sampled-row parity:
+    ``config2_65k`` (65,536 x 32 heads resident in HBM and streamed from
+    pinned DRAM with a 1 GiB workspace) and ``config4_paged`` (158,208 x 48
+    heads from a 256-token page store).  Returns False when one of them
+    failed its parity; an error inside one is recorded in its entry."""
+    legs = [leg for leg in args.side_workloads.split(",") if leg and leg != "none"]
+    ok = True
+    for leg in legs:
+        key, measure = {"65k": ("config2_65k", measure_65k), "paged": ("config4_paged", measure_paged)}[leg]
+        log(f"side workload {leg}: {args.side_steps} steps after {args.side_warmup} warmup")
+        t0 = time.perf_counter()
+        try:
+            entry = measure(args, args.side_steps, args.side_warmup, h2d_peak=h2d_peak)
+        except Exception as error:  # noqa: BLE001 - reported in the line, the headline stands
+            entry = {"error": f"{type(error).__name__}: {error}"}
+            release_memory()
+        else:
+            entry = {k: v for k, v in entry.items() if k not in _SIDE_DROP}
+            ok = ok and (entry.get("parity") is None or bool(entry["parity"].get("ok")))
+        entry["wall_seconds"] = round(time.perf_counter() - t0, 1)
+        result[key] = entry
+        log(f"side workload {leg} done in {entry['wall_seconds']} s")
+    return ok
+
+
+def oracle_sample(q, k, v, rows, kv_chunk, workers, scale=None):
+    """Oracle O and LSE of query ``rows`` over all keys (one segment) and the
+    seconds it took: (ref_o, ref_l, seconds)."""
     import numpy as np
     import torch
     from threadpoolctl import threadpool_limits
@@ -511,7 +562,23 @@ def sampled_parity(q, k, v, out, lse, rows, kv_chunk, workers, scale=None):
         ref_o, ref_l = chunked_attention(u16(q[rows]), u16(k), u16(v), [0, rows.size], [0, n],
                                          q_chunk_tokens=rows.size, kv_chunk_tokens=kv_chunk,
                                          softmax_scale=scale, workers=workers)
-    cpu_s = time.perf_counter() - t0
+    return ref_o, ref_l, time.perf_counter() - t0
+
+
+def sampled_parity(q, k, v, out, lse, rows, kv_chunk, workers, scale=None):
+    """Oracle O (and LSE) on sampled query rows against the GPU result; also
+    the CPU baseline timing (returns parity dict, seconds)."""
+    ref_o, ref_l, cpu_s = oracle_sample(q, k, v, rows, kv_chunk, workers, scale)
+    return compare_sample(out, lse, rows, ref_o, ref_l), cpu_s
+
+
+def compare_sample(out, lse, rows, ref_o, ref_l) -> dict:
+    """Parity of the GPU result's ``rows`` against the oracle's: O max-abs <=
+    2e-2, relative L2 <= 5e-3, every element within 2^-5 (|ref| + rms), LSE
+    max-abs <= 1e-3."""
+    import numpy as np
+    import torch
+
     idx = torch.from_numpy(rows)
     got = (out[idx.to(out.device)] if out.device.type == "cuda" else out[idx]).float().cpu().numpy()
     diff = np.abs(got - ref_o)
@@ -526,7 +593,7 @@ def sampled_parity(q, k, v, out, lse, rows, kv_chunk, workers, scale=None):
         parity["max_abs_lse"] = float(np.abs(got_l - ref_l).max())
         ok = ok and parity["max_abs_lse"] <= 1e-3
     parity["ok"] = bool(ok)
-    return parity, cpu_s
+    return parity
 
 
 def run_pinned(q, k, v, cu, budget_gib, kv_chunk, steps, warmup, lse=None, output_mode="host", out=None):
@@ -567,24 +634,44 @@ def sweep_main(args) -> int:
     q, k, v = make_inputs(n, h, d, args.seed)
     import torch
 
+    import numpy as np
+
     cu = torch.tensor([0, n], dtype=torch.int32)
     rows = []
     published = {1: 206.3, 2: 217.4, 4: 218.5, 8: 218.2, 14: 218.9}  # README.md:61-68 (RTX 5090)
+    # Sampled-row parity of every point: the reference's signature rows plus
+    # seeded-random rows, every head, all keys, against the oracle chunking
+    # K/V like the point's plan (computed once per K/V chunk size).
+    rng = np.random.default_rng(args.seed)
+    sample = np.unique(np.concatenate([[0, n // 4, n // 2, 3 * n // 4, n - 1],
+                                       rng.choice(n, args.parity_rows, replace=False)]))
+    oracle = {}
     # One page-locked output for all budgets, and each budget's workspace
     # returned to the device before the next is allocated, so every point
     # starts from the same host and device memory state.
     host_out = torch.empty((n, h, d), dtype=q.dtype, pin_memory=True)
+    lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
+    all_ok = True
     for gib in (1, 2, 4, 8, 14):
         gc.collect()
         torch.cuda.empty_cache()
-        plan, out, stats, sec = run_pinned(q, k, v, cu, gib, None, args.steps, args.warmup, out=host_out)
+        plan, out, stats, sec = run_pinned(q, k, v, cu, gib, None, args.steps, args.warmup, lse=lse, out=host_out)
         tflops = flop / sec / 1e12
+        h2d_gbps = stats.h2d_bytes / args.steps / sec / 1e9
         rows.append({"workspace_gib": gib, "q_chunk_tokens": plan.q_chunk_tokens,
                      "kv_chunk_tokens": plan.kv_chunk_tokens, "q_passes": plan.q_passes,
                      "h2d_gib_per_step": round(stats.h2d_bytes / args.steps / 2**30, 1),
                      "seconds_per_step": round(sec, 3), "tflops": round(tflops, 1),
-                     "h2d_gbps": round(stats.h2d_bytes / args.steps / sec / 1e9, 1),
+                     "mfma_peak_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
+                     "h2d_gbps": round(h2d_gbps, 1), "h2d_frac": round(h2d_gbps / h2d_peak, 4),
                      "published_rtx5090_tflops": published[gib]})
+        if not args.no_parity:
+            if plan.kv_chunk_tokens not in oracle:
+                log(f"sweep: oracle on {sample.size} rows x {h} heads, K/V chunk {plan.kv_chunk_tokens}")
+                oracle[plan.kv_chunk_tokens] = oracle_sample(q, k, v, sample, plan.kv_chunk_tokens,
+                                                             args.cpu_workers)[:2]
+            rows[-1]["parity"] = compare_sample(out, lse, sample, *oracle[plan.kv_chunk_tokens])
+            all_ok = all_ok and rows[-1]["parity"]["ok"]
         log(f"sweep {gib} GiB: {rows[-1]}")
         del out
     two = next(r for r in rows if r["workspace_gib"] == 2)
@@ -598,9 +685,10 @@ def sweep_main(args) -> int:
                                "pinned DRAM incl. final D2H; value at the 2 GiB workspace"},
         "h2d_measured_gbps": round(h2d_peak, 1),
         "sweep": rows,
+        "parity_ok": all_ok if not args.no_parity else None,
     }
     print(json.dumps(result), flush=True)
-    return 0
+    return 0 if all_ok else 1
 
 
 def million_main(args) -> int:
@@ -666,30 +754,37 @@ def million_main(args) -> int:
 def small_main(args) -> int:
     """65,536 tokens x 32 heads x 128: fully resident in HBM and streamed
     from pinned DRAM with a 1 GiB workspace and 4,096-token K/V chunks."""
+    result = measure_65k(args, args.steps, args.warmup, h2d_peak=measure_h2d_gbps())
+    print(json.dumps(result), flush=True)
+    return 0 if (result["parity"] is None or result["parity"]["ok"]) else 1
+
+
+def measure_65k(args, steps, warmup, h2d_peak=None) -> dict:
+    """The 65,536-token workload's result line (see small_main)."""
     import numpy as np
     import torch
 
-    from seqattn import StreamingAttentionConfig, StreamingAttentionRunner, build_plan
+    from seqattn import StreamingAttentionConfig, StreamingAttentionRunner
 
     n, h, d = 65_536, 32, 128
     flop = 4 * h * d * n * n
     q, k, v = make_inputs(n, h, d, args.seed)
     cu = torch.tensor([0, n], dtype=torch.int32)
     lse_s = torch.empty((h, n), dtype=torch.float32, device="cuda")
-    plan, out_s, stats, sec_s = run_pinned(q, k, v, cu, 1, 4096, args.steps, args.warmup, lse=lse_s)
+    plan, out_s, stats, sec_s = run_pinned(q, k, v, cu, 1, 4096, steps, warmup, lse=lse_s)
     config = StreamingAttentionConfig(workspace_budget_bytes=2**30, kv_chunk_tokens=4096, backend="hip")
     runner = StreamingAttentionRunner(plan, config)
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     out_r = torch.empty_like(qd)
     lse_r = torch.empty_like(lse_s)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         runner(qd, kd, vd, cu, cu, out=out_r, lse_out=lse_r)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         runner(qd, kd, vd, cu, cu, out=out_r, lse_out=lse_r)
     torch.cuda.synchronize()
-    sec_r = (time.perf_counter() - t0) / args.steps
+    sec_r = (time.perf_counter() - t0) / steps
     identical = bool(torch.equal(out_r.cpu(), out_s) and torch.equal(lse_r, lse_s))
     parity = cpu_baseline = None
     if not args.no_parity:
@@ -702,23 +797,29 @@ def small_main(args) -> int:
         cpu_baseline = {"value": 4 * h * d * rows.size * n / cpu_s / 1e12, "unit": "TFLOPS",
                         "cores": args.cpu_workers, "kind": "port",
                         "sample": f"{rows.size} query rows x {h} heads x all {n} keys; {cpu_s:.2f} s"}
+    h2d_gbps = stats.h2d_bytes / steps / sec_s / 1e9
     result = {
         "metric": "effective TFLOPS, 65K-tok BF16 MHA, resident in HBM and streamed with 1 GiB",
-        "value": round(flop / sec_r / 1e12, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps,
-        "warmup": args.warmup, "ms_per_step": round(sec_r * 1e3, 2), "higher_is_better": True,
+        "value": round(flop / sec_r / 1e12, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": steps,
+        "warmup": warmup, "ms_per_step": round(sec_r * 1e3, 2), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: Q/K/V ~ N(0,1) bf16 seeded per 4,096-token chunk",
         "config": {"workload": f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}; value: Q/K/V "
                                "resident in HBM; streamed: pinned DRAM with a 1 GiB workspace, K/V chunk 4,096",
                    "q_chunk_tokens": plan.q_chunk_tokens, "q_passes": plan.q_passes},
+        "mfma_peak_frac": round(flop / sec_r / 1e12 / PEAK_BF16_TFLOPS, 4),
         "streamed_1gib": {"tflops": round(flop / sec_s / 1e12, 2), "ms_per_step": round(sec_s * 1e3, 2),
-                          "h2d_gb_per_step": round(stats.h2d_bytes / args.steps / 1e9, 2)},
+                          "mfma_peak_frac": round(flop / sec_s / 1e12 / PEAK_BF16_TFLOPS, 4),
+                          "h2d_gb_per_step": round(stats.h2d_bytes / steps / 1e9, 2),
+                          "h2d_achieved_gbps": round(h2d_gbps, 2),
+                          "h2d_frac": round(h2d_gbps / h2d_peak, 4) if h2d_peak else None},
         "cpu_baseline": cpu_baseline,
         "parity": parity,
     }
-    print(json.dumps(result), flush=True)
     runner.close()
-    return 0 if (parity is None or parity["ok"]) else 1
+    del q, k, v, qd, kd, vd, out_r, out_s, lse_r, lse_s, runner
+    release_memory()
+    return result
 
 
 PROJ_TOKENS, PROJ_HIDDEN, PROJ_HEADS, PROJ_HEAD_DIM = 61_312, 5_376, 56, 128
@@ -856,6 +957,13 @@ def paged_main(args) -> int:
     mode).  A step is one full paged run from the store: the K/V pages are
     read from the store once (first Q block) and served from the page cache
     for the later Q blocks; writing the store is data preparation, untimed."""
+    result = measure_paged(args, args.steps, args.warmup, h2d_peak=measure_h2d_gbps())
+    print(json.dumps(result), flush=True)
+    return 0 if (result["parity"] is None or result["parity"]["ok"]) else 1
+
+
+def measure_paged(args, steps, warmup, h2d_peak=None) -> dict:
+    """The paged workload's result line (see paged_main)."""
     import tempfile
 
     import numpy as np
@@ -903,18 +1011,18 @@ def paged_main(args) -> int:
         kv_pages = store.kv_pages
         out = torch.empty((n, h, d), dtype=torch.bfloat16, device="cuda")
         lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
-        for i in range(args.warmup):
+        for i in range(warmup):
             runner.run_with_device_output(store, store, cu, cu, out=out, lse_out=lse)
             torch.cuda.synchronize()
-            log(f"paged: warmup {i + 1}/{args.warmup} done")
+            log(f"paged: warmup {i + 1}/{warmup} done")
         stats = PagedAttentionStats()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for i in range(args.steps):
+        for i in range(steps):
             runner.run_with_device_output(store, store, cu, cu, out=out, lse_out=lse, stats=stats)
-            log(f"paged: step {i + 1}/{args.steps} done")
+            log(f"paged: step {i + 1}/{steps} done")
         torch.cuda.synchronize()
-        sec = (time.perf_counter() - t0) / args.steps
+        sec = (time.perf_counter() - t0) / steps
     tflops = flop / sec / 1e12
     log(f"paged: {tflops:.1f} effective TFLOPS, {sec:.3f} s/step")
 
@@ -974,7 +1082,7 @@ def paged_main(args) -> int:
                         "sample": f"{rows.size} query rows x {h} heads x all {n} keys; {cpu_s:.1f} s; numpy "
                                   f"float32, heads split over {args.cpu_workers} threads"}
         log(f"paged parity: {parity}")
-    steps = args.steps
+    h2d_gbps = stats.h2d_bytes / steps / sec / 1e9
     result = {
         "metric": "effective TFLOPS, paged 158K-tok BF16 MHA, 256-token pages from an aligned page store"
                   + (", INT8 K/V pages" if storage == "int8" else ""),
@@ -982,7 +1090,7 @@ def paged_main(args) -> int:
         "unit": "TFLOPS",
         "n_gpus": 1,
         "steps": steps,
-        "warmup": args.warmup,
+        "warmup": warmup,
         "ms_per_step": round(sec * 1e3, 2),
         "higher_is_better": True,
         "scaling": "weak",
@@ -1007,6 +1115,8 @@ def paged_main(args) -> int:
             "store_read_gb_per_step": round(stats.nvme_physical_read_bytes / steps / 1e9, 3),
             "store_read_seconds_per_step": round(stats.nvme_read_seconds / steps, 3),
             "h2d_gb_per_step": round(stats.h2d_bytes / steps / 1e9, 3),
+            "h2d_achieved_gbps": round(h2d_gbps, 2),
+            "h2d_frac": round(h2d_gbps / h2d_peak, 4) if h2d_peak else None,
             "gpu_kernel_seconds_per_step": round(stats.gpu_kernel_seconds / steps, 3),
             "io_queue_wait_seconds_per_step": round(stats.io_queue_wait_seconds / steps, 3),
             "operator_host_peak_bytes": stats.operator_host_peak_bytes,
@@ -1015,8 +1125,10 @@ def paged_main(args) -> int:
         "cpu_baseline": cpu_baseline,
         "parity": parity,
     }
-    print(json.dumps(result), flush=True)
-    return 0 if (parity is None or parity["ok"]) else 1
+    # Each paged run releases its own workspace, cache and stages when it ends.
+    del q, k, v, out, lse, runner
+    release_memory()
+    return result
 
 
 if __name__ == "__main__":
