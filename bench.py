@@ -90,6 +90,9 @@ def parse_args():
                          "inputs resident in HBM (reported beside it)")
     ap.add_argument("--resident-steps", type=int, default=3,
                     help="timed steps of the HBM-resident leg (at most --steps)")
+    ap.add_argument("--aliased-steps", type=int, default=2,
+                    help="timed steps of the host_aliased leg (output finalized into the Q block; at most "
+                         "--steps; 0 skips it)")
     ap.add_argument("--resident-warmup", type=int, default=1,
                     help="warmup steps of the HBM-resident leg (at most --warmup)")
     ap.add_argument("--traffic-file", type=Path,
@@ -312,6 +315,21 @@ def main() -> int:
     lib = _native.lib()
     handle = runner._workspace.handle
 
+    # Sampled rows of the parity check: the reference's signature rows plus
+    # seeded-random rows.  Each leg's O and LSE on them are kept as it ends.
+    rng = np.random.default_rng(args.seed)
+    signature = np.array([0, n // 4, n // 2, 3 * n // 4, n - 1])
+    rows = np.unique(np.concatenate([signature, rng.choice(n, args.parity_rows, replace=False)]))
+    rows_t = torch.from_numpy(rows)
+    legs_out = []
+
+    def keep_rows(leg, out, lse):
+        # Snapshots for the parity check; with --no-parity nothing is read
+        # back (no torch kernels run in a profiled process).
+        if not args.no_parity:
+            idx = rows_t if out.device.type == "cpu" else rows_t.cuda()
+            legs_out.append((leg, out[idx].cpu(), lse[:, rows_t.cuda()].cpu()))
+
     # Headline: caller-owned pinned DRAM -> 2 GiB workspace -> pinned DRAM.
     out_host = torch.empty((n, h, d), dtype=torch.bfloat16, pin_memory=True)
     lse_pinned = torch.empty((h, n), dtype=torch.float32, device="cuda")
@@ -341,6 +359,7 @@ def main() -> int:
     }
     log(f"pinned DRAM e2e: {value:.1f} TFLOPS, {sec:.3f} s/step, kernel busy {busy_per_step_ms:.1f} ms/step "
         f"({kernel_tflops:.1f} TFLOPS), H2D {pcie['h2d_achieved_gbps']:.1f} GB/s")
+    keep_rows("pinned", out_host, lse_pinned)
 
     resident = None
     out_dev = lse_res = None
@@ -368,8 +387,58 @@ def main() -> int:
             "workload": "same inputs resident in HBM (no PCIe), V read through a transposed copy, "
                         "one update launch per step with the finalize fused",
         }
-        del qd, kd, vd
+        keep_rows("resident", out_dev, lse_res)
+        del qd, kd, vd, out_dev
+        release_memory()
         log(f"resident: {resident['value']:.1f} TFLOPS, {r_sec:.3f} s/step")
+
+    aliased = None
+    if args.aliased_steps > 0:
+        # The same pinned-DRAM step with output_mode="host_aliased": each
+        # pass's output is finalized into its own Q block, so the budget
+        # holds no output slot, the Q block is larger and there are fewer
+        # passes over K/V (less H2D).  Same inputs, same output buffer.
+        a_config = StreamingAttentionConfig(workspace_budget_bytes=int(args.workspace_gib * 2**30),
+                                            kv_chunk_tokens=args.kv_chunk, output_mode="host_aliased",
+                                            backend="hip")
+        a_plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
+                            max_q_tokens=n, max_kv_tokens=n, config=a_config)
+        a_runner = StreamingAttentionRunner(a_plan, a_config)
+        a_stats = StreamingAttentionStats()
+        a_lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
+        a_steps = min(args.aliased_steps, args.steps)
+        a_warm = min(1, args.warmup)
+        a_sec, a_busy, _, a_launches = timed_steps(
+            lib, a_runner._workspace.handle,
+            lambda i: a_runner(q, k, v, cu, cu, out=out_host, lse_out=a_lse, stats=a_stats if i is not None else None),
+            a_steps, a_warm, "aliased",
+        )
+        a_h2d = a_stats.h2d_bytes / a_steps
+        aliased = {
+            "value": round(flop / a_sec / 1e12, 2),
+            "unit": "TFLOPS",
+            "ms_per_step": round(a_sec * 1e3, 2),
+            "steps": a_steps,
+            "warmup": a_warm,
+            "mfma_peak_frac": round(flop / a_sec / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "kernel_tflops": round(flop / (a_busy / a_steps / 1e3) / 1e12, 2) if a_busy > 0 else None,
+            "q_chunk_tokens": a_plan.q_chunk_tokens,
+            "kv_chunk_tokens": a_plan.kv_chunk_tokens,
+            "q_passes": a_plan.q_passes,
+            "estimated_workspace_bytes": a_plan.estimated_workspace_bytes,
+            "update_launches_per_step": a_launches // a_steps,
+            "h2d_gb_per_step": round(a_h2d / 1e9, 2),
+            "h2d_achieved_gbps": round(a_h2d / a_sec / 1e9, 2),
+            "h2d_frac": round(a_h2d / a_sec / 1e9 / h2d_peak, 4),
+            "workload": "same pinned-DRAM step and 2 GiB budget with output_mode='host_aliased' (output "
+                        "finalized into the pass's Q block, no output slot)",
+        }
+        keep_rows("aliased", out_host, a_lse)
+        a_runner.close()
+        del a_runner, a_lse
+        release_memory()
+        log(f"aliased: {aliased['value']:.1f} TFLOPS, {a_sec:.3f} s/step, {a_plan.q_passes} passes, "
+            f"H2D {aliased['h2d_achieved_gbps']:.1f} GB/s")
 
     parity = None
     cpu_baseline = None
@@ -378,9 +447,6 @@ def main() -> int:
 
         from oracle.seqattn_oracle import chunked_attention
 
-        rng = np.random.default_rng(args.seed)
-        signature = np.array([0, n // 4, n // 2, 3 * n // 4, n - 1])
-        rows = np.unique(np.concatenate([signature, rng.choice(n, args.parity_rows, replace=False)]))
         threads = args.cpu_workers
         log(f"oracle on {rows.size} rows x {h} heads x {n} keys, {threads} threads")
         # bf16 bit patterns as uint16 views of the pinned host tensors (no copy)
@@ -394,13 +460,9 @@ def main() -> int:
                 kv_chunk_tokens=plan.kv_chunk_tokens, causal=False, workers=threads,
             )
         cpu_s = time.perf_counter() - t0
-        rows_t = torch.from_numpy(rows)
         errors, rel_l2, scaled, lse_err = {}, {}, {}, {}
         ref_norm = float(np.linalg.norm(ref_o))
         rms = ref_norm / math.sqrt(ref_o.size)
-        legs_out = [("pinned", out_host[rows_t], lse_pinned[:, rows_t.cuda()].cpu())]
-        if out_dev is not None:
-            legs_out.append(("resident", out_dev[rows_t.cuda()].cpu(), lse_res[:, rows_t.cuda()].cpu()))
         for leg, got, got_l in legs_out:
             diff = np.abs(got.float().numpy() - ref_o)
             errors[leg] = float(diff.max())
@@ -408,8 +470,9 @@ def main() -> int:
             scaled[leg] = float((diff / (np.abs(ref_o) + rms)).max())
             lse_err[leg] = float(np.abs(got_l.numpy() - ref_l).max())
         identical = None
-        if len(legs_out) == 2:
-            identical = bool(torch.equal(legs_out[0][1], legs_out[1][1]) and torch.equal(legs_out[0][2], legs_out[1][2]))
+        if len(legs_out) > 1:
+            identical = all(torch.equal(legs_out[0][1], got) and torch.equal(legs_out[0][2], got_l)
+                            for _, got, got_l in legs_out[1:])
         err_o, err_l = max(errors.values()), max(lse_err.values())
         parity = {
             "rows": int(rows.size),
@@ -500,6 +563,7 @@ def main() -> int:
         },
         "pcie": pcie,
         "resident_hbm": resident,
+        "host_aliased": aliased,
         "cpu_baseline": cpu_baseline,
         "parity": parity,
     }
@@ -507,7 +571,7 @@ def main() -> int:
     # buffers before the side workloads (and before the interpreter shuts
     # down).
     runner.close()
-    del out_host, out_dev, lse_pinned, lse_res, q, k, v, runner
+    del out_host, lse_pinned, lse_res, q, k, v, runner, legs_out
     release_memory()
     side_ok = run_side_workloads(args, result, h2d_peak)
     print(json.dumps(result), flush=True)
