@@ -22,11 +22,14 @@ two concurrent launches, one per half of the Q block's rows, on two streams.
 * cpu_baseline: the CPU oracle (numpy restatement of the reference's chunked
   FP32 attention) timed on this host on a bounded row sample, which is also
   the parity check of the sampled rows (O and LSE) of both legs;
-* config2_65k and config4_paged: the benchmark's other configurations,
-  measured after the headline leg's buffers are released (65,536 tokens x
-  32 heads resident and streamed with 1 GiB; 158,208 tokens x 48 heads from
-  a 256-token page store), each with TFLOPS, MFMA-peak and PCIe fractions and
-  its own sampled-row parity.
+* host_aliased: the same pinned step with each pass's output finalized
+  into its Q block (no output slot in the budget, 14 passes instead of 19);
+* config2_65k, config4_paged and config5_1m: the benchmark's other
+  configurations, measured after the headline leg's buffers are released
+  (65,536 tokens x 32 heads resident and streamed with 1 GiB; 158,208
+  tokens x 48 heads from a 256-token page store; 1,048,576 tokens x 64
+  heads with peaked keys and an 8 GiB workspace, one step), each with
+  TFLOPS, MFMA-peak and PCIe fractions and its own sampled-row parity.
 
 Effective TFLOPS = 4 * heads * head_dim * tokens^2 / seconds per step (the
 reference's definition, benchmarking/streaming.py:206).  Prints ONE JSON line.
@@ -104,9 +107,9 @@ def parse_args():
                          "heads, peaked scores, 8 GiB workspace, with LSE; 65k: 65,536 tokens x 32 heads "
                          "resident in HBM and streamed with 1 GiB; projected: 61,312 tokens of hidden "
                          "size 5,376 through QKV projection, attention and output projection")
-    ap.add_argument("--side-workloads", default="65k,paged",
+    ap.add_argument("--side-workloads", default="65k,paged,1m",
                     help="streamed workload: other configurations measured after the headline leg and "
-                         "reported as keys of the same line (65k, paged; 'none' for neither)")
+                         "reported as keys of the same line (65k, paged, 1m; 'none' for none)")
     ap.add_argument("--side-steps", type=int, default=3, help="timed steps of each side workload")
     ap.add_argument("--side-warmup", type=int, default=1, help="warmup steps of each side workload")
     ap.add_argument("--kv-storage", default="bf16", choices=["bf16", "int8"],
@@ -243,7 +246,7 @@ def timed_steps(lib, handle, step, steps, warmup, label):
     t0 = time.perf_counter()
     for i in range(steps):
         step(i)
-        log(f"{label}: step {i + 1}/{steps} enqueued")
+        log(f"{label}: step {i + 1}/{steps} returned at {time.perf_counter() - t0:.3f} s")
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     busy, total, count = ctypes.c_double(), ctypes.c_double(), ctypes.c_int64()
@@ -587,17 +590,22 @@ def run_side_workloads(args, result, h2d_peak) -> bool:
     """The other configurations of the benchmark, measured in the same
     process after the headline leg, each with its sampled-row parity:
     ``config2_65k`` (65,536 x 32 heads resident in HBM and streamed from
-    pinned DRAM with a 1 GiB workspace) and ``config4_paged`` (158,208 x 48
-    heads from a 256-token page store).  Returns False when one of them
+    pinned DRAM with a 1 GiB workspace), ``config4_paged`` (158,208 x 48
+    heads from a 256-token page store) and ``config5_1m`` (1,048,576 x 64
+    heads, peaked keys, 8 GiB workspace, one step).  Returns False when one of them
     failed its parity; an error inside one is recorded in its entry."""
     legs = [leg for leg in args.side_workloads.split(",") if leg and leg != "none"]
     ok = True
     for leg in legs:
-        key, measure = {"65k": ("config2_65k", measure_65k), "paged": ("config4_paged", measure_paged)}[leg]
-        log(f"side workload {leg}: {args.side_steps} steps after {args.side_warmup} warmup")
+        key, measure = {"65k": ("config2_65k", measure_65k), "paged": ("config4_paged", measure_paged),
+                        "1m": ("config5_1m", measure_1m)}[leg]
+        # The 1M-token run is about 30 s per step: one step, no warmup
+        # (its kernels are already loaded by the headline legs).
+        steps, warmup = (1, 0) if leg == "1m" else (args.side_steps, args.side_warmup)
+        log(f"side workload {leg}: {steps} steps after {warmup} warmup")
         t0 = time.perf_counter()
         try:
-            entry = measure(args, args.side_steps, args.side_warmup, h2d_peak=h2d_peak)
+            entry = measure(args, steps, warmup, h2d_peak=h2d_peak)
         except Exception as error:  # noqa: BLE001 - reported in the line, the headline stands
             entry = {"error": f"{type(error).__name__}: {error}"}
             release_memory()
@@ -758,12 +766,18 @@ def sweep_main(args) -> int:
 def million_main(args) -> int:
     """1,048,576 tokens x 64 heads x 128 from pinned DRAM, 8 GiB workspace,
     K/V chunk 8,192; K scaled per head by U[0.5, 4] (peaked scores); LSE on."""
+    result = measure_1m(args, args.steps, args.warmup, h2d_peak=measure_h2d_gbps())
+    print(json.dumps(result), flush=True)
+    return 0 if (result["parity"] is None or result["parity"]["ok"]) else 1
+
+
+def measure_1m(args, steps, warmup, h2d_peak=None) -> dict:
+    """The 1,048,576-token workload's result line (see million_main)."""
     import numpy as np
     import torch
 
     n, h, d = 1_048_576, 64, 128
     flop = 4 * h * d * n * n
-    h2d_peak = measure_h2d_gbps()
     log("1m: generating inputs")
     q, k, v = make_inputs(n, h, d, args.seed)
     head_scale = torch.from_numpy(np.random.default_rng(args.seed + 11).uniform(0.5, 4.0, size=h)).to(torch.float32)
@@ -780,8 +794,9 @@ def million_main(args) -> int:
         out = torch.empty((n, h, d), dtype=torch.bfloat16)
         out_kind = "pageable host memory (page-locking a fourth 16 GiB buffer failed)"
     log(f"1m: output in {out_kind}")
-    plan, out, stats, sec = run_pinned(q, k, v, cu, 8, 8192, args.steps, args.warmup, lse=lse, out=out)
+    plan, out, stats, sec = run_pinned(q, k, v, cu, 8, 8192, steps, warmup, lse=lse, out=out)
     tflops = flop / sec / 1e12
+    h2d_gbps = stats.h2d_bytes / steps / sec / 1e9
     log(f"1m: {tflops:.1f} TFLOPS, {sec:.2f} s/step, passes {plan.q_passes}")
     parity = cpu_baseline = None
     if not args.no_parity:
@@ -795,7 +810,7 @@ def million_main(args) -> int:
         log(f"1m parity: {parity}")
     result = {
         "metric": "effective TFLOPS, 1M-tok BF16 MHA from pinned DRAM, 8 GiB HBM",
-        "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "value": round(tflops, 2), "unit": "TFLOPS", "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(sec * 1e3, 1), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: Q, V ~ N(0,1); K ~ N(0,1) x per-head U[0.5, 4]; bf16, seeded per 4,096-token chunk",
@@ -805,14 +820,16 @@ def million_main(args) -> int:
                    "q_chunk_tokens": plan.q_chunk_tokens, "kv_chunk_tokens": plan.kv_chunk_tokens,
                    "q_passes": plan.q_passes},
         "mfma_peak_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
-        "pcie": {"h2d_gb_per_step": round(stats.h2d_bytes / args.steps / 1e9, 1),
-                 "h2d_achieved_gbps": round(stats.h2d_bytes / args.steps / sec / 1e9, 1),
-                 "h2d_measured_gbps": round(h2d_peak, 1)},
+        "pcie": {"h2d_gb_per_step": round(stats.h2d_bytes / steps / 1e9, 1),
+                 "h2d_achieved_gbps": round(h2d_gbps, 1),
+                 "h2d_measured_gbps": round(h2d_peak, 1) if h2d_peak else None,
+                 "h2d_frac": round(h2d_gbps / h2d_peak, 4) if h2d_peak else None},
         "cpu_baseline": cpu_baseline,
         "parity": parity,
     }
-    print(json.dumps(result), flush=True)
-    return 0 if (parity is None or parity["ok"]) else 1
+    del q, k, v, out, lse
+    release_memory()
+    return result
 
 
 def small_main(args) -> int:
