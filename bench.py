@@ -327,8 +327,7 @@ def main() -> int:
     legs_out = []
 
     def keep_rows(leg, out, lse):
-        # Snapshots for the parity check; with --no-parity nothing is read
-        # back (no torch kernels run in a profiled process).
+        # Snapshots for the parity check; with --no-parity nothing is read back.
         if not args.no_parity:
             idx = rows_t if out.device.type == "cpu" else rows_t.cuda()
             legs_out.append((leg, out[idx].cpu(), lse[:, rows_t.cuda()].cpu()))
