@@ -81,6 +81,8 @@ def parse_args():
     ap.add_argument("--workspace-gib", type=float, default=2.0)
     ap.add_argument("--output-mode", default="host", choices=["host", "host_aliased"])
     ap.add_argument("--kv-chunk", type=int, default=None)
+    ap.add_argument("--num-kv-buffers", type=int, default=None,
+                    help="K/V ring slots (1-3; default: the planner's 2)")
     ap.add_argument("--parity-rows", type=int, default=1024,
                     help="seeded-random query rows checked against the CPU oracle (plus 5 signature rows); "
                          "the same oracle run is the timed CPU baseline")
@@ -309,6 +311,7 @@ def main() -> int:
         kv_chunk_tokens=args.kv_chunk,
         output_mode=args.output_mode,
         backend="hip",
+        **({} if args.num_kv_buffers is None else {"num_kv_buffers": args.num_kv_buffers}),
     )
     plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
                       max_q_tokens=n, max_kv_tokens=n, config=config)
@@ -542,6 +545,7 @@ def main() -> int:
             "output_mode": args.output_mode,
             "q_chunk_tokens": plan.q_chunk_tokens,
             "kv_chunk_tokens": plan.kv_chunk_tokens,
+            "num_kv_buffers": plan.num_kv_buffers,
             "q_passes": plan.q_passes,
             "rows_per_pass": rows_per_pass,
             "estimated_workspace_bytes": plan.estimated_workspace_bytes,
