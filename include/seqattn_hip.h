@@ -201,8 +201,12 @@ int32_t sa_pipeline_destroy(sa_pipeline* pipeline);
  * for each segment, for each Q super-block: Q H2D on the H2D stream, then per
  * K/V chunk an H2D into the next ring slot (fenced by that slot's free event)
  * and an update launch on compute_stream (fenced by the slot's ready event),
- * then finalize into an output slot and D2H into out_host on the D2H stream.
- * Returns after the D2H stream has drained.
+ * then the finalized block is copied into out_host on the D2H stream.  With
+ * one output slot (or none, output_mode host_aliased) the block's last chunk
+ * launches write the output and the LSE in their epilogue, into the buffer
+ * that held the block's Q, in place of a state store and a finalize launch;
+ * with two slots a finalize launch writes the output slot.  Returns after
+ * the D2H stream has drained.
  *
  *   q_host/k_host/v_host/out_host: contiguous pinned host [tokens, heads, head_dim] dtype
  *   cu_seqlens_q/k: num_segments + 1 host int64 boundaries
