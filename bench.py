@@ -5,8 +5,8 @@ head_dim 128, Q/K/V ~ N(0,1) (seeded per 4,096-token chunk like the reference
 benchmark) in caller-owned pinned DRAM, output back to caller-owned pinned
 DRAM, through a 2 GiB HBM workspace in the decomposition the planner picks:
 resident Q blocks of 28,416 tokens, 8,192-token K/V chunks, 19 passes over
-K/V, the final D2H included (the reference's benchmarking/streaming.py:188-213
-setting).  The LSE of every row is written too.  Each K/V chunk is applied by
+K/V, the final D2H included (the reference's
+src/seqattn_core/benchmarking/streaming.py:185-213 setting).  The LSE of every row is written too.  Each K/V chunk is applied by
 two concurrent launches, one per half of the Q block's rows, on two streams.
 
 ``value`` is that pinned-DRAM step.  Beside it, from the same run:
@@ -32,7 +32,7 @@ two concurrent launches, one per half of the Q block's rows, on two streams.
   TFLOPS, MFMA-peak and PCIe fractions and its own sampled-row parity.
 
 Effective TFLOPS = 4 * heads * head_dim * tokens^2 / seconds per step (the
-reference's definition, benchmarking/streaming.py:206).  Prints ONE JSON line.
+reference's definition, src/seqattn_core/benchmarking/streaming.py:206).  Prints ONE JSON line.
 """
 
 from __future__ import annotations
@@ -129,7 +129,8 @@ def parse_args():
 
 def make_inputs(tokens, heads, head_dim, seed, chunk_tokens=4096, workers=16, pinned=True):
     """Q/K/V (page-locked by default) filled per 4,096-token chunk from generators
-    seeded seed + tensor * 1,000,003 + chunk (reference benchmarking/common.py:47-73)."""
+    seeded seed + tensor * 1,000,003 + chunk (reference
+    src/seqattn_core/benchmarking/common.py:45-71)."""
     import torch
     from concurrent.futures import ThreadPoolExecutor
 

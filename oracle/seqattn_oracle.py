@@ -259,7 +259,8 @@ def brute_force_row(q_row, k_seg, v_seg, *, scale, visible_keys=None):
 
 def seeded_normal_chunks(tokens: int, heads: int, head_dim: int, *, seed: int, tensor_index: int,
                          chunk_tokens: int = 4096, dtype=None):
-    """Input tensor as the reference benchmark fills it (benchmarking/common.py:47-73).
+    """Input tensor as the reference benchmark fills it
+    (src/seqattn_core/benchmarking/common.py:45-71).
 
     Chunk c of tensor t is ``normal_`` from a CPU generator seeded with
     ``seed + t * 1_000_003 + c``.  Returns a torch tensor (the generator

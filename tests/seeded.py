@@ -1,6 +1,7 @@
 """Seeded inputs and sampled-row parity checks for the GPU configuration tests.
 
-Inputs follow the reference benchmark's scheme (benchmarking/common.py:47-73):
+Inputs follow the reference benchmark's scheme
+(src/seqattn_core/benchmarking/common.py:45-71):
 chunk c (4,096 tokens) of tensor t is ``normal_`` from a CPU generator seeded
 with ``seed + t * 1_000_003 + c``; here the chunks are filled by a thread
 pool straight into page-locked tensors.
