@@ -121,6 +121,9 @@ def parse_args():
                     help="paged: directory for the temporary page store (default: $TMPDIR)")
     ap.add_argument("--direct-io", default="auto", choices=["auto", "on", "off"],
                     help="paged: O_DIRECT store I/O (auto: on when the filesystem supports it)")
+    ap.add_argument("--ceiling-seconds", type=float, default=5.0,
+                    help="streamed workload: seconds of each sustained-rate reference measured after the "
+                         "legs (the register-only MFMA probe and the vendor bf16 GEMM); 0 skips them")
     ap.add_argument("--hbm-copy-calibration", type=float, default=None, metavar="GIB",
                     help="only run one device-to-device copy of GIB GiB and exit: the known-size copy "
                          "whose FETCH_SIZE / WRITE_SIZE counters scale the update kernel's counters")
@@ -170,6 +173,78 @@ def measure_h2d_gbps(nbytes=2 * 2**30, repeats=3):
     torch.cuda.empty_cache()
     torch._C._host_emptyCache()  # return the page-locked probe buffer to the OS
     return best
+
+
+def measure_ceilings(seconds: float) -> dict:
+    """Sustained bf16 matrix-core rates of this GPU, measured in this process
+    after the attention legs (the chip is warm): the register-only MFMA probe
+    (libseqattn_probe.so: MFMAs on register operands, no memory traffic, no
+    other VALU work) and the vendor library's bf16 GEMM (torch.matmul, which
+    dispatches to hipBLASLt) at 16384^3 with B transposed, the layout of
+    Q.K^T (both operands contiguous along the reduction).  Each is the median
+    over batches of about 0.5 s during `seconds`."""
+    import ctypes
+
+    import torch
+
+    def median_rate(run_batch, flop_per_batch):
+        rates = []
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            run_batch()
+            e1.record()
+            e1.synchronize()
+            rates.append(flop_per_batch / (e0.elapsed_time(e1) / 1e3) / 1e12)
+        rates.sort()
+        return rates[len(rates) // 2], len(rates)
+
+    out = {"seconds_each": seconds}
+    probe_path = ROOT / "stream-attn_amd" / "seqattn" / "_lib" / "libseqattn_probe.so"
+    probe = ctypes.CDLL(str(probe_path))
+    probe.sa_probe_mfma_out_elems.restype = ctypes.c_int64
+    probe.sa_probe_mfma_flop_per_launch.restype = ctypes.c_double
+    probe.sa_probe_mfma.restype = ctypes.c_int32
+    probe.sa_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32,
+                                    ctypes.c_void_p]
+    elems = probe.sa_probe_mfma_out_elems()
+    buf = torch.empty(elems, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream().cuda_stream
+    per_launch = probe.sa_probe_mfma_flop_per_launch()
+    launches = max(1, int(0.5 / (per_launch / 2.0e15)))
+
+    def probe_batch():
+        if probe.sa_probe_mfma(buf.data_ptr(), elems, launches, 1, stream) != 0:
+            raise RuntimeError("sa_probe_mfma failed")
+
+    probe_batch()
+    torch.cuda.synchronize()
+    rate, batches = median_rate(probe_batch, per_launch * launches)
+    out["mfma_register_only_tflops"] = round(rate, 1)
+    out["mfma_register_only"] = (f"v_mfma_f32_16x16x32_bf16 on register operands, 8 waves per CU (two per "
+                                 f"SIMD), {launches} launches per batch, median of {batches} batches")
+    del buf
+    n = 16384
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    c = torch.empty(n, n, device="cuda", dtype=torch.bfloat16)
+    calls = 40
+
+    def gemm_batch():
+        for _ in range(calls):
+            torch.matmul(a, b.t(), out=c)
+
+    torch.matmul(a, b.t(), out=c)
+    torch.cuda.synchronize()
+    rate, batches = median_rate(gemm_batch, 2 * n ** 3 * calls)
+    out["vendor_gemm_tflops"] = round(rate, 1)
+    out["vendor_gemm"] = (f"torch.matmul(A, B.t()) bf16 {n}x{n}x{n} (hipBLASLt), {calls} calls per batch, "
+                          f"median of {batches} batches")
+    del a, b, c
+    torch.cuda.empty_cache()
+    return out
 
 
 def hbm_copy_calibration(gib: float) -> int:
@@ -583,6 +658,18 @@ def main() -> int:
     runner.close()
     del out_host, lse_pinned, lse_res, q, k, v, runner, legs_out
     release_memory()
+    if args.ceiling_seconds > 0:
+        log("sustained-rate references: register-only MFMA probe and vendor bf16 GEMM")
+        ceilings = measure_ceilings(args.ceiling_seconds)
+        gemm = ceilings["vendor_gemm_tflops"]
+        ceilings["pinned_kernel_vs_gemm"] = round(kernel_tflops / gemm, 4) if kernel_tflops else None
+        r_kernel = resident.get("kernel_tflops") if resident else None
+        ceilings["resident_kernel_vs_gemm"] = round(r_kernel / gemm, 4) if r_kernel else None
+        ceilings["value_vs_gemm"] = round(value / gemm, 4)
+        result["ceilings"] = ceilings
+        log(f"ceilings: MFMA register-only {ceilings['mfma_register_only_tflops']:.0f} TFLOPS, vendor GEMM "
+            f"{gemm:.0f} TFLOPS; update kernel at {ceilings['pinned_kernel_vs_gemm']} (pinned) and "
+            f"{ceilings['resident_kernel_vs_gemm']} (resident) of the GEMM rate")
     side_ok = run_side_workloads(args, result, h2d_peak)
     print(json.dumps(result), flush=True)
     return 0 if (parity is None or parity["ok"]) and side_ok else 1

@@ -19,9 +19,12 @@ CSRC = PACKAGE_ROOT / "csrc"
 INCLUDE = REPO_ROOT / "include"
 LIB_DIR = PACKAGE_ROOT / "seqattn" / "_lib"
 LIB_PATH = LIB_DIR / "libseqattn_hip.so"
+# bench.py's register-only MFMA rate probe; not part of the attention path.
+PROBE_LIB_PATH = LIB_DIR / "libseqattn_probe.so"
 ARCH = "gfx950"
 
 SOURCES = ("sa_kernels.hip", "sa_pipeline.cpp")
+PROBE_SOURCES = ("sa_probe.hip",)
 
 # Device-side flags.  Packed FP32 VALU instructions are disabled for all
 # device code.
@@ -50,16 +53,23 @@ def hipcc() -> str:
 
 
 def build(verbose: bool = False) -> Path:
-    """Compile every source and link the shared library; returns its path."""
+    """Compile every source into the attention library and the probe library;
+    returns the attention library's path."""
+    _link(SOURCES, LIB_PATH, verbose)
+    _link(PROBE_SOURCES, PROBE_LIB_PATH, verbose)
+    return LIB_PATH
+
+
+def _link(sources, target: Path, verbose: bool) -> None:
     LIB_DIR.mkdir(parents=True, exist_ok=True)
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+    tmp = target.with_suffix(".so.tmp")
     cmd = [
         hipcc(),
         *HIP_FLAGS,
         f"-I{INCLUDE}",
         f"-I{CSRC}",
         "-shared",
-        *(str(CSRC / name) for name in SOURCES),
+        *(str(CSRC / name) for name in sources),
         "-o",
         str(tmp),
     ]
@@ -75,8 +85,7 @@ def build(verbose: bool = False) -> Path:
         raise RuntimeError(f"hipcc failed ({result.returncode}):\n{stderr}")
     if verbose and stderr.strip():
         print(stderr, file=sys.stderr)
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, target)
 
 
 if __name__ == "__main__":

@@ -334,12 +334,15 @@ struct SideJoin {
 // launch then writes acc / l and the LSE in its epilogue instead of storing
 // the state, with the finalize kernel's expressions, and *fused_done is set.
 // The caller runs the finalize kernel itself when no launch was made.
+// `prefetched_slot`, if not -1, is the ring slot into which prefetch_chunk
+// already copied the span's first chunk (and recorded its kv_ready event).
 int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, const KVSource& src,
                    int32_t kv_tokens, int32_t kv_local_offset, bool* initialize,
                    int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
                    int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
                    const std::function<int32_t(int32_t)>* after_copy = nullptr,
-                   const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr) {
+                   const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr,
+                   int32_t prefetched_slot = -1) {
   if (kv_tokens < 0 || kv_local_offset < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad K/V span kv_tokens=%d kv_local_offset=%d q_tokens=%d", kv_tokens,
                   kv_local_offset, q_tokens);
@@ -393,9 +396,10 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
       if (rc != 0) return rc;
       add_stats(st, 0, 0, 0, 1, 0);
     } else {
-      const int slot = (int)(p->ring_next++ % p->num_kv);
+      const bool prefetched = start == 0 && prefetched_slot >= 0;
+      const int slot = prefetched ? prefetched_slot : (int)(p->ring_next++ % p->num_kv);
       const int64_t bytes = (int64_t)n * p->kv_row_bytes;
-      {
+      if (!prefetched) {
         TraceRange range(p->trace, "seqattn:kv_h2d");
         int32_t wrc = wait_slot_free(p, slot);
         if (wrc != 0) return wrc;
@@ -404,8 +408,8 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
         SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], src.v + (int64_t)start * p->kv_row_bytes,
                                      bytes, hipMemcpyHostToDevice, p->h2d));
         SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
+        add_stats(st, 2 * bytes, 0, 0, 1, 0);
       }
-      add_stats(st, 2 * bytes, 0, 0, 1, 0);
       if (after_copy) {
         const int32_t hrc = (*after_copy)(start / p->kv_chunk);
         if (hrc != 0) return hrc;
@@ -544,12 +548,35 @@ int32_t init_state(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, in
                       SA_FLAG_INITIALIZE, compute);
 }
 
+// Copy the first K/V chunk (rows [0, n) of k_host / v_host) of a span into
+// the next ring slot now; stream_kv then launches on it without copying
+// (prefetched_slot).  In host_aliased runs the next Q block's copy has to
+// wait until the previous block's output has left the Q buffer, and the H2D
+// stream runs in order, so a first chunk copied after the Q block would wait
+// too; copied before it, the chunk lands while the previous block's last
+// chunk still computes.
+int32_t prefetch_chunk(sa_pipeline* p, const void* k_host, const void* v_host, int32_t n,
+                       sa_pipeline_stats* st, int32_t* slot_out) {
+  const int slot = (int)(p->ring_next++ % p->num_kv);
+  const int64_t bytes = (int64_t)n * p->kv_row_bytes;
+  TraceRange range(p->trace, "seqattn:kv_h2d");
+  int32_t rc = wait_slot_free(p, slot);
+  if (rc != 0) return rc;
+  SA_HIP_RETURN(hipMemcpyAsync(p->k_slots[slot], k_host, bytes, hipMemcpyHostToDevice, p->h2d));
+  SA_HIP_RETURN(hipMemcpyAsync(p->v_slots[slot], v_host, bytes, hipMemcpyHostToDevice, p->h2d));
+  SA_HIP_RETURN(hipEventRecord(p->kv_ready[slot], p->h2d));
+  add_stats(st, 2 * bytes, 0, 0, 1, 0);
+  *slot_out = slot;
+  return 0;
+}
+
 int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_t k_length,
                   int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
                   int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
                   const void* q_block = nullptr,
                   const std::function<int32_t(int32_t)>* after_copy = nullptr,
-                  const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr) {
+                  const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr,
+                  int32_t prefetched_slot = -1) {
   if (k_length < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad stream_kv sizes k_length=%d q_tokens=%d", k_length, q_tokens);
     return SA_ERR_INVALID_ARGUMENT;
@@ -559,7 +586,8 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
   KVSource src{static_cast<const char*>(k_host), static_cast<const char*>(v_host), false, 0, 0, 0, 0};
   bool initialize = true;
   int32_t rc = apply_span(p, q, qt, p->head_dim, src, k_length, 0, &initialize, q_tokens, q_local_offset,
-                          causal_shift, scale, causal, compute, st, after_copy, fused_last, fused_done);
+                          causal_shift, scale, causal, compute, st, after_copy, fused_last, fused_done,
+                          prefetched_slot);
   if (rc != 0) return rc;
   if (initialize)
     return init_state(p, q, qt, p->head_dim, q_tokens, q_local_offset, causal_shift, scale, compute);
@@ -1296,7 +1324,14 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
     const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
     for (int64_t qt = q_start; qt < q_stop; qt += block) {
       const int32_t n = (int32_t)std::min<int64_t>(block, q_stop - qt);
-      int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
+      int32_t rc = 0;
+      int32_t prefetched_slot = -1;
+      if (!p->has_out_slots && k_length > 0) {
+        rc = prefetch_chunk(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
+                            (int32_t)std::min<int64_t>(p->kv_chunk, k_length), stats, &prefetched_slot);
+        if (rc) return rc;
+      }
+      rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
       if (rc) return rc;
       // Without output slots the block is finalized into the Q buffer, which
       // the last chunk launches do themselves in their epilogue.
@@ -1306,7 +1341,7 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
       rc = stream_kv(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
                      (int32_t)k_length, n, (int32_t)(qt - q_start), causal_shift, softmax_scale,
                      causal, compute, stats, nullptr, nullptr, p->has_out_slots ? nullptr : &fused,
-                     &fused_done);
+                     &fused_done, prefetched_slot);
       if (rc) return rc;
       const int32_t slot = (int32_t)(chunk_index % p->num_out);
       const int64_t bytes = (int64_t)n * p->q_row_bytes;

@@ -113,9 +113,9 @@ def check(lib, label):
 
 
 def run_tensor_mode(lib, *, num_kv, num_out, causal, q_lengths, k_lengths, q_chunk=1024, kv_chunk=256,
-                    q_heads=4, kv_heads=2, head_dim=64, with_lse=True):
+                    q_heads=4, kv_heads=2, head_dim=64, with_lse=True, out_slots=True):
     p = Pipeline(lib, q_chunk=q_chunk, kv_chunk=kv_chunk, q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim,
-                 num_kv=num_kv, num_out=num_out)
+                 num_kv=num_kv, num_out=num_out, out_slots=out_slots)
     host = Space(0x5000_0000_0000)
     cu_q, q_b = bounds(q_lengths)
     cu_k, k_b = bounds(k_lengths)
@@ -154,6 +154,20 @@ def test_tensor_mode_schedule_is_race_free(ledger, num_kv, num_out, causal):
         assert counts[0] > 0 and counts[1] > 0 and counts[2] > 0
         assert stats.d2h_bytes == sum(q_lengths) * 4 * 64 * HEAD_BYTES
         check(ledger, f"num_kv={num_kv} num_out={num_out} causal={causal} q={q_lengths} k={k_lengths}")
+
+
+@pytest.mark.parametrize("num_kv", [1, 2, 3])
+@pytest.mark.parametrize("causal", [False, True])
+def test_host_aliased_schedule_is_race_free(ledger, num_kv, causal):
+    # output_mode="host_aliased": no output slot; each block is finalized
+    # into the Q buffer and copied out from it, and the next block's first
+    # K/V chunk is copied before its Q block.
+    for q_lengths, k_lengths in CASES:
+        ledger.ledger_reset()
+        stats = run_tensor_mode(ledger, num_kv=num_kv, num_out=1, causal=causal, q_lengths=q_lengths,
+                                k_lengths=k_lengths, out_slots=False)
+        assert stats.d2h_bytes == sum(q_lengths) * 4 * 64 * HEAD_BYTES
+        check(ledger, f"host_aliased num_kv={num_kv} causal={causal} q={q_lengths} k={k_lengths}")
 
 
 def test_step_api_schedules_are_race_free(ledger):
@@ -214,7 +228,7 @@ def test_resident_schedule_with_transposed_v_scratch_is_race_free(ledger):
 def test_a_dropped_wait_is_reported(ledger):
     # Every stream wait of one run is dropped in turn.  The waits that keep a
     # K/V slot, the Q block / output slot pair or the D2H ordered are
-    # necessary, so most drops must be reported (65 of 69 here); the rest are
+    # necessary, so most drops must be reported (63 of 69 here); the rest are
     # waits another ordering already implies.
     def run():
         run_tensor_mode(ledger, num_kv=2, num_out=1, causal=False, q_lengths=[3000], k_lengths=[1100])
@@ -232,4 +246,29 @@ def test_a_dropped_wait_is_reported(ledger):
         assert ledger.ledger_dropped() == 1
         caught += ledger.ledger_check(None, 0) > 0
     print(f"dropped-wait runs reported: {caught} of {waits}")
+    assert caught >= waits * 3 // 4
+
+
+def test_a_dropped_wait_is_reported_in_host_aliased_runs(ledger):
+    # The same mutation check for the host_aliased schedule, whose Q block
+    # doubles as the output buffer: the waits that keep the next block's Q
+    # copy behind the previous block's output copy, and the prefetched first
+    # chunk behind the slot's last readers, must be among those reported.
+    def run():
+        run_tensor_mode(ledger, num_kv=2, num_out=1, causal=False, q_lengths=[3000], k_lengths=[1100],
+                        out_slots=False)
+
+    ledger.ledger_reset()
+    run()
+    check(ledger, "baseline")
+    waits = ledger.ledger_waits()
+    assert waits > 10
+    caught = 0
+    for n in range(waits):
+        ledger.ledger_reset()
+        ledger.ledger_drop_wait(n)
+        run()
+        assert ledger.ledger_dropped() == 1
+        caught += ledger.ledger_check(None, 0) > 0
+    print(f"host_aliased dropped-wait runs reported: {caught} of {waits}")
     assert caught >= waits * 3 // 4

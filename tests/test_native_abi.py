@@ -130,3 +130,27 @@ def test_noalloc_entry_point_rejects_bad_arguments_before_touching_the_gpu():
     assert call([0, 1, 2], [0, 131_072, 131_072 + 131_073]) == -1
     message = lib.sa_last_error()
     assert b"segment 1 needs" in message and b"67108864" in message
+
+
+PROBE_HEADER = HEADER.parent / "seqattn_probe.h"
+PROBE_LIB = Path(_native.LIB_PATH).parent / "libseqattn_probe.so"
+
+
+@pytest.mark.skipif(not PROBE_LIB.exists(), reason="probe library not built")
+def test_probe_library_exports_every_declared_symbol():
+    import ctypes
+
+    names = re.findall(r"^\s*(?:int32_t|int64_t|double)\s+(sa_probe_\w+)\s*\(", PROBE_HEADER.read_text(), re.M)
+    assert sorted(names) == ["sa_probe_mfma", "sa_probe_mfma_flop_per_launch", "sa_probe_mfma_out_elems"]
+    lib = ctypes.CDLL(str(PROBE_LIB))
+    for name in names:
+        assert hasattr(lib, name), name
+    lib.sa_probe_mfma_out_elems.restype = ctypes.c_int64
+    lib.sa_probe_mfma_flop_per_launch.restype = ctypes.c_double
+    elems = lib.sa_probe_mfma_out_elems()
+    assert elems == 256 * 8 * 512
+    assert lib.sa_probe_mfma_flop_per_launch() == 256 * 8 * 8 * 2048 * 24 * 16 * 16 * 32 * 2
+    # A null or undersized buffer is rejected before anything is enqueued.
+    lib.sa_probe_mfma.argtypes = [ctypes.c_void_p, ctypes.c_int64, ctypes.c_int32, ctypes.c_uint32, ctypes.c_void_p]
+    assert lib.sa_probe_mfma(None, elems, 1, 0, None) == -1
+    assert lib.sa_probe_mfma(ctypes.c_void_p(16), elems - 1, 1, 0, None) == -1
