@@ -154,6 +154,11 @@ struct sa_pipeline {
   // slot take turns as a pass's Q block and output (ready: Q copied in;
   // done: output finalized; free: output copied out).
   hipEvent_t alt_ready[2] = {}, alt_done[2] = {}, alt_free[2] = {};
+  // sa_pipeline_run without output slots (host_aliased): per row piece of
+  // the Q block, its output written (done), copied out (out) and the next
+  // block's Q rows copied in (ready).
+  static constexpr int kPieces = 4;
+  hipEvent_t piece_done[kPieces] = {}, piece_out[kPieces] = {}, piece_ready[kPieces] = {};
   bool q_pending = false;
   bool kv_pending[3] = {false, false, false};
   bool out_pending[2] = {false, false};
@@ -198,6 +203,11 @@ void release(sa_pipeline* p) {
     if (p->alt_ready[i]) (void)hipEventDestroy(p->alt_ready[i]);
     if (p->alt_done[i]) (void)hipEventDestroy(p->alt_done[i]);
     if (p->alt_free[i]) (void)hipEventDestroy(p->alt_free[i]);
+  }
+  for (int i = 0; i < sa_pipeline::kPieces; ++i) {
+    if (p->piece_done[i]) (void)hipEventDestroy(p->piece_done[i]);
+    if (p->piece_out[i]) (void)hipEventDestroy(p->piece_out[i]);
+    if (p->piece_ready[i]) (void)hipEventDestroy(p->piece_ready[i]);
   }
   for (hipEvent_t e : p->t_start) (void)hipEventDestroy(e);
   for (hipEvent_t e : p->t_stop) (void)hipEventDestroy(e);
@@ -334,15 +344,12 @@ struct SideJoin {
 // launch then writes acc / l and the LSE in its epilogue instead of storing
 // the state, with the finalize kernel's expressions, and *fused_done is set.
 // The caller runs the finalize kernel itself when no launch was made.
-// `prefetched_slot`, if not -1, is the ring slot into which prefetch_chunk
-// already copied the span's first chunk (and recorded its kv_ready event).
 int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, const KVSource& src,
                    int32_t kv_tokens, int32_t kv_local_offset, bool* initialize,
                    int32_t q_tokens, int32_t q_local_offset, int32_t causal_shift, double scale,
                    int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
                    const std::function<int32_t(int32_t)>* after_copy = nullptr,
-                   const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr,
-                   int32_t prefetched_slot = -1) {
+                   const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr) {
   if (kv_tokens < 0 || kv_local_offset < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad K/V span kv_tokens=%d kv_local_offset=%d q_tokens=%d", kv_tokens,
                   kv_local_offset, q_tokens);
@@ -396,10 +403,9 @@ int32_t apply_span(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, co
       if (rc != 0) return rc;
       add_stats(st, 0, 0, 0, 1, 0);
     } else {
-      const bool prefetched = start == 0 && prefetched_slot >= 0;
-      const int slot = prefetched ? prefetched_slot : (int)(p->ring_next++ % p->num_kv);
+      const int slot = (int)(p->ring_next++ % p->num_kv);
       const int64_t bytes = (int64_t)n * p->kv_row_bytes;
-      if (!prefetched) {
+      {
         TraceRange range(p->trace, "seqattn:kv_h2d");
         int32_t wrc = wait_slot_free(p, slot);
         if (wrc != 0) return wrc;
@@ -548,13 +554,8 @@ int32_t init_state(sa_pipeline* p, const void* q, int64_t sq_t, int64_t sq_h, in
                       SA_FLAG_INITIALIZE, compute);
 }
 
-// Copy the first K/V chunk (rows [0, n) of k_host / v_host) of a span into
-// the next ring slot now; stream_kv then launches on it without copying
-// (prefetched_slot).  In host_aliased runs the next Q block's copy has to
-// wait until the previous block's output has left the Q buffer, and the H2D
-// stream runs in order, so a first chunk copied after the Q block would wait
-// too; copied before it, the chunk lands while the previous block's last
-// chunk still computes.
+// Copy K/V rows [0, n) of k_host / v_host into the next ring slot (after its
+// last readers) and record its kv_ready event; *slot_out names the slot.
 int32_t prefetch_chunk(sa_pipeline* p, const void* k_host, const void* v_host, int32_t n,
                        sa_pipeline_stats* st, int32_t* slot_out) {
   const int slot = (int)(p->ring_next++ % p->num_kv);
@@ -575,8 +576,7 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
                   int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
                   const void* q_block = nullptr,
                   const std::function<int32_t(int32_t)>* after_copy = nullptr,
-                  const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr,
-                  int32_t prefetched_slot = -1) {
+                  const sa::FusedOutput* fused_last = nullptr, bool* fused_done = nullptr) {
   if (k_length < 0 || q_tokens < 0 || q_tokens > p->q_chunk) {
     sa::set_error("bad stream_kv sizes k_length=%d q_tokens=%d", k_length, q_tokens);
     return SA_ERR_INVALID_ARGUMENT;
@@ -586,8 +586,7 @@ int32_t stream_kv(sa_pipeline* p, const void* k_host, const void* v_host, int32_
   KVSource src{static_cast<const char*>(k_host), static_cast<const char*>(v_host), false, 0, 0, 0, 0};
   bool initialize = true;
   int32_t rc = apply_span(p, q, qt, p->head_dim, src, k_length, 0, &initialize, q_tokens, q_local_offset,
-                          causal_shift, scale, causal, compute, st, after_copy, fused_last, fused_done,
-                          prefetched_slot);
+                          causal_shift, scale, causal, compute, st, after_copy, fused_last, fused_done);
   if (rc != 0) return rc;
   if (initialize)
     return init_state(p, q, qt, p->head_dim, q_tokens, q_local_offset, causal_shift, scale, compute);
@@ -762,6 +761,155 @@ int32_t run_alternating(sa_pipeline* p, const char* qh, const char* kh, const ch
   return 0;
 }
 
+// sa_pipeline_run without output slots (output_mode="host_aliased").  A
+// pass's output is written into its own Q block and copied out from there,
+// and the next pass's Q block is copied into the same buffer, so between two
+// passes the block crosses the link twice while no update can run on it.
+// That boundary is worked in row pieces of the block (multiples of the
+// update kernel's workgroup tile):
+//  - the pass's last K/V chunk is applied to one piece at a time, and each
+//    piece's output is copied out as soon as its launch ends;
+//  - the next pass's first K/V chunk is copied before its Q block, and its Q
+//    rows of a piece are copied in as soon as the output rows they overwrite
+//    have left;
+//  - that first chunk is applied to each piece as its Q rows land.
+// The chunks in between are applied to the whole block (apply_span).  Every
+// row sees the same chunks in the same order as with one launch per chunk,
+// so the results are bit-identical.
+int32_t run_aliased(sa_pipeline* p, const char* qh, const char* kh, const char* vh, char* oh, float* lse,
+                    int64_t lse_sh, const std::vector<Pass>& passes, double scale, int32_t causal,
+                    hipStream_t compute, sa_pipeline_stats* st) {
+  constexpr int kP = sa_pipeline::kPieces;
+  if (passes.empty()) return 0;
+  const int32_t tile = sa::update_block_rows(p->head_dim);
+  const int64_t q_stride = (int64_t)p->q_heads * p->head_dim;
+  const int64_t kt = (int64_t)p->kv_heads * p->head_dim;
+  char* qbuf = static_cast<char*>(p->q_buffer);
+  // Row bounds r[0..np] of the pieces of an n-row block (n > 0).
+  auto piece_bounds = [&](int32_t n, int32_t* r) -> int {
+    const int32_t tiles = (n + tile - 1) / tile;
+    const int np = std::max(1, std::min(kP, (int)tiles));
+    for (int j = 0; j <= np; ++j)
+      r[j] = j == np ? n : std::min<int32_t>(n, (int32_t)((int64_t)tiles * j / np) * tile);
+    return np;
+  };
+  // Work another entry point left on the Q buffer completes first.
+  if (p->q_pending) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->q_free, 0));
+  int32_t r_out[kP + 1] = {};
+  int np_out = 0;  // pieces whose output copies are the last enqueued (0: none)
+  auto copy_q = [&](const Pass& ps, const int32_t* r, int np) -> int32_t {
+    TraceRange range(p->trace, "seqattn:q_h2d");
+    for (int j = 0; j < np; ++j) {
+      if (np_out > 0) {
+        // The output copies run in order on the D2H stream: waiting for the
+        // last one that overlaps rows [r[j], r[j+1]) covers all of them.
+        int k = 0;
+        while (k + 1 < np_out && r_out[k + 1] < r[j + 1]) ++k;
+        SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->piece_out[k], 0));
+      }
+      const int64_t bytes = (int64_t)(r[j + 1] - r[j]) * p->q_row_bytes;
+      if (bytes > 0)
+        SA_HIP_RETURN(hipMemcpyAsync(qbuf + r[j] * p->q_row_bytes, qh + (ps.qt + r[j]) * p->q_row_bytes, bytes,
+                                     hipMemcpyHostToDevice, p->h2d));
+      SA_HIP_RETURN(hipEventRecord(p->piece_ready[j], p->h2d));
+    }
+    add_stats(st, (int64_t)ps.n * p->q_row_bytes, 0, 1, 0, ps.n);
+    return 0;
+  };
+  // One chunk of K/V rows [start, start + n_k) of pass ps, applied to each
+  // piece on the compute stream.  first: each piece first waits for its Q
+  // rows; last: each piece writes its output (and LSE) and records
+  // piece_done.
+  auto pieces_chunk = [&](const Pass& ps, const int32_t* r, int np, int slot, int32_t start, int32_t n_k,
+                          bool first, bool last) -> int32_t {
+    SA_HIP_RETURN(hipStreamWaitEvent(compute, p->kv_ready[slot], 0));
+    const int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | (first ? SA_FLAG_INITIALIZE : 0);
+    for (int j = 0; j < np; ++j) {
+      if (first) SA_HIP_RETURN(hipStreamWaitEvent(compute, p->piece_ready[j], 0));
+      const sa::FusedOutput fused{qbuf + r[j] * p->q_row_bytes, q_stride, p->head_dim, lse, lse_sh, ps.qt + r[j]};
+      const int32_t rc = launch_timed(p, qbuf + r[j] * p->q_row_bytes, q_stride, p->head_dim, p->k_slots[slot], kt,
+                                      p->head_dim, p->v_slots[slot], kt, p->head_dim, r[j + 1] - r[j], n_k,
+                                      ps.q_local + r[j], start, ps.causal_shift, scale, flags, compute, 0,
+                                      last ? &fused : nullptr, r[j]);
+      if (rc != 0) return rc;
+      if (last) SA_HIP_RETURN(hipEventRecord(p->piece_done[j], compute));
+    }
+    SA_HIP_RETURN(hipEventRecord(p->kv_free[slot], compute));
+    p->kv_pending[slot] = true;
+    p->kv_side_pending[slot] = false;
+    return 0;
+  };
+  int32_t rc = 0;
+  int32_t r[kP + 1], r_next[kP + 1];
+  int np = piece_bounds(passes[0].n, r);
+  int32_t slot0 = -1;
+  rc = prefetch_chunk(p, kh + passes[0].k_start * p->kv_row_bytes, vh + passes[0].k_start * p->kv_row_bytes,
+                      std::min<int32_t>(p->kv_chunk, passes[0].k_len), st, &slot0);
+  if (rc) return rc;
+  if ((rc = copy_q(passes[0], r, np)) != 0) return rc;
+  for (size_t i = 0; i < passes.size(); ++i) {
+    const Pass& ps = passes[i];
+    const bool has_next = i + 1 < passes.size();
+    // Chunks the block applies: the first always, later ones while some row
+    // of the block can see them (bottom-right causal rule).
+    const int64_t visible_end =
+        causal ? std::max<int64_t>(0, (int64_t)ps.q_local + ps.n + ps.causal_shift) : INT64_MAX;
+    int32_t last_start = 0;
+    for (int32_t start = p->kv_chunk; start < ps.k_len && start < visible_end; start += p->kv_chunk)
+      last_start = start;
+    const int32_t n_first = std::min<int32_t>(p->kv_chunk, ps.k_len);
+    const bool single = last_start == 0;
+    if ((rc = pieces_chunk(ps, r, np, slot0, 0, n_first, true, single)) != 0) return rc;
+    if (!single) {
+      if (last_start > p->kv_chunk) {
+        KVSource src{kh + (ps.k_start + p->kv_chunk) * p->kv_row_bytes,
+                     vh + (ps.k_start + p->kv_chunk) * p->kv_row_bytes, false, 0, 0, 0, 0};
+        bool initialize = false;
+        rc = apply_span(p, qbuf, q_stride, p->head_dim, src, last_start - p->kv_chunk, p->kv_chunk, &initialize,
+                        ps.n, ps.q_local, ps.causal_shift, scale, causal, compute, st);
+        if (rc) return rc;
+      }
+      int32_t slot = -1;
+      rc = prefetch_chunk(p, kh + (ps.k_start + last_start) * p->kv_row_bytes,
+                          vh + (ps.k_start + last_start) * p->kv_row_bytes,
+                          std::min<int32_t>(p->kv_chunk, ps.k_len - last_start), st, &slot);
+      if (rc) return rc;
+      rc = pieces_chunk(ps, r, np, slot, last_start, std::min<int32_t>(p->kv_chunk, ps.k_len - last_start), false,
+                        true);
+      if (rc) return rc;
+    }
+    int np_next = 0;
+    if (has_next) {
+      const Pass& nx = passes[i + 1];
+      np_next = piece_bounds(nx.n, r_next);
+      rc = prefetch_chunk(p, kh + nx.k_start * p->kv_row_bytes, vh + nx.k_start * p->kv_row_bytes,
+                          std::min<int32_t>(p->kv_chunk, nx.k_len), st, &slot0);
+      if (rc) return rc;
+    }
+    {
+      TraceRange range(p->trace, "seqattn:output_d2h");
+      for (int j = 0; j < np; ++j) {
+        SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->piece_done[j], 0));
+        const int64_t bytes = (int64_t)(r[j + 1] - r[j]) * p->q_row_bytes;
+        if (bytes > 0)
+          SA_HIP_RETURN(hipMemcpyAsync(oh + (ps.qt + r[j]) * p->q_row_bytes, qbuf + r[j] * p->q_row_bytes, bytes,
+                                       hipMemcpyDeviceToHost, p->d2h));
+        SA_HIP_RETURN(hipEventRecord(p->piece_out[j], p->d2h));
+      }
+      add_stats(st, 0, (int64_t)ps.n * p->q_row_bytes, 0, 0, 0);
+    }
+    np_out = np;
+    std::copy(r, r + np + 1, r_out);
+    if (has_next) {
+      if ((rc = copy_q(passes[i + 1], r_next, np_next)) != 0) return rc;
+      np = np_next;
+      std::copy(r_next, r_next + np_next + 1, r);
+    }
+  }
+  SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -879,6 +1027,11 @@ int32_t sa_pipeline_create(sa_pipeline** out_pipeline, int32_t device, void* q_b
     err = hipEventCreateWithFlags(&p->alt_ready[i], flags);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&p->alt_done[i], flags);
     if (err == hipSuccess) err = hipEventCreateWithFlags(&p->alt_free[i], flags);
+  }
+  for (int i = 0; i < sa_pipeline::kPieces && err == hipSuccess; ++i) {
+    err = hipEventCreateWithFlags(&p->piece_done[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->piece_out[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->piece_ready[i], flags);
   }
   if (err != hipSuccess) {
     int32_t rc = sa::hip_status(err, "sa_pipeline_create stream/event creation");
@@ -1294,7 +1447,7 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
   const char* kh = static_cast<const char*>(k_host);
   const char* vh = static_cast<const char*>(v_host);
   char* oh = static_cast<char*>(out_host);
-  if (p->has_out_slots && p->num_out == 1) {
+  if (!p->has_out_slots || p->num_out == 1) {
     std::vector<Pass> passes;
     for (int32_t s = 0; s < num_segments; ++s) {
       const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
@@ -1309,6 +1462,8 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
         passes.push_back(Pass{qt, k_start, (int32_t)std::min<int64_t>(block, q_stop - qt), (int32_t)k_length,
                               (int32_t)(qt - q_start), (int32_t)(k_length - q_length)});
     }
+    if (!p->has_out_slots)
+      return run_aliased(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
     return run_alternating(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
   }
   int64_t chunk_index = 0;
@@ -1324,38 +1479,19 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
     const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
     for (int64_t qt = q_start; qt < q_stop; qt += block) {
       const int32_t n = (int32_t)std::min<int64_t>(block, q_stop - qt);
-      int32_t rc = 0;
-      int32_t prefetched_slot = -1;
-      if (!p->has_out_slots && k_length > 0) {
-        rc = prefetch_chunk(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
-                            (int32_t)std::min<int64_t>(p->kv_chunk, k_length), stats, &prefetched_slot);
-        if (rc) return rc;
-      }
-      rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
+      // Two output slots: the block is finalized into slot i % 2 and copied
+      // out while the next block streams.
+      int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
       if (rc) return rc;
-      // Without output slots the block is finalized into the Q buffer, which
-      // the last chunk launches do themselves in their epilogue.
-      const int64_t q_stride = (int64_t)p->q_heads * p->head_dim;
-      const sa::FusedOutput fused{p->q_buffer, q_stride, p->head_dim, lse, lse_stride_h, qt};
-      bool fused_done = false;
       rc = stream_kv(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
                      (int32_t)k_length, n, (int32_t)(qt - q_start), causal_shift, softmax_scale,
-                     causal, compute, stats, nullptr, nullptr, p->has_out_slots ? nullptr : &fused,
-                     &fused_done, prefetched_slot);
+                     causal, compute, stats);
       if (rc) return rc;
       const int32_t slot = (int32_t)(chunk_index % p->num_out);
       const int64_t bytes = (int64_t)n * p->q_row_bytes;
-      if (p->has_out_slots) {
-        rc = finalize(p, slot, n, lse, lse_stride_h, qt, compute);
-        if (rc) return rc;
-        rc = d2h(p, oh + qt * p->q_row_bytes, p->out_slots[slot], bytes, slot, 0, compute, stats);
-      } else {
-        if (!fused_done) {
-          rc = finalize(p, -1, n, lse, lse_stride_h, qt, compute);
-          if (rc) return rc;
-        }
-        rc = d2h(p, oh + qt * p->q_row_bytes, p->q_buffer, bytes, slot, 1, compute, stats);
-      }
+      rc = finalize(p, slot, n, lse, lse_stride_h, qt, compute);
+      if (rc) return rc;
+      rc = d2h(p, oh + qt * p->q_row_bytes, p->out_slots[slot], bytes, slot, 0, compute, stats);
       if (rc) return rc;
       ++chunk_index;
     }
