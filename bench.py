@@ -124,6 +124,10 @@ def parse_args():
     ap.add_argument("--ceiling-seconds", type=float, default=5.0,
                     help="streamed workload: seconds of each sustained-rate reference measured after the "
                          "legs (the register-only MFMA probe and the vendor bf16 GEMM); 0 skips them")
+    ap.add_argument("--maps-out", type=Path, default=None, metavar="PATH",
+                    help="copy /proc/self/maps to PATH when the interpreter exits (before shared-library "
+                         "destructors run), so that a crash in a destructor after the result line can be "
+                         "mapped to the library it happened in")
     ap.add_argument("--hbm-copy-calibration", type=float, default=None, metavar="GIB",
                     help="only run one device-to-device copy of GIB GiB and exit: the known-size copy "
                          "whose FETCH_SIZE / WRITE_SIZE counters scale the update kernel's counters")
@@ -336,6 +340,11 @@ def timed_steps(lib, handle, step, steps, warmup, label):
 
 def main() -> int:
     args = parse_args()
+    if args.maps_out is not None:
+        import atexit
+        import shutil
+
+        atexit.register(shutil.copyfile, "/proc/self/maps", args.maps_out)
     if args.gpus != 1:
         print(
             f"bench.py measures one GPU; --gpus {args.gpus} is not supported (the streamed path is "
