@@ -205,8 +205,13 @@ int32_t sa_pipeline_destroy(sa_pipeline* pipeline);
  * one output slot (or none, output_mode host_aliased) the block's last chunk
  * launches write the output and the LSE in their epilogue, into the buffer
  * that held the block's Q, in place of a state store and a finalize launch;
- * with two slots a finalize launch writes the output slot.  Returns after
- * the D2H stream has drained.
+ * with two slots a finalize launch writes the output slot.  Without output
+ * slots the block's output leaves, and the next block's Q rows arrive, in
+ * row pieces of the block (multiples of the update kernel's workgroup tile)
+ * as the block's last chunk launches finish piece by piece, and the next
+ * block's first chunk is copied ahead of its Q rows and applied to each
+ * piece as its rows land; every row still sees the same chunks in the same
+ * order.  Returns after the D2H stream has drained.
  *
  *   q_host/k_host/v_host/out_host: contiguous pinned host [tokens, heads, head_dim] dtype
  *   cu_seqlens_q/k: num_segments + 1 host int64 boundaries

@@ -170,6 +170,19 @@ def test_host_aliased_schedule_is_race_free(ledger, num_kv, causal):
         check(ledger, f"host_aliased num_kv={num_kv} causal={causal} q={q_lengths} k={k_lengths}")
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_host_aliased_pieces_at_head_dim_128_are_race_free(ledger, causal):
+    # The GPU test's shapes: 384-row workgroup tiles, blocks of 3-4 tiles
+    # (3-4 pieces), a segment with fewer keys than queries and one with fewer
+    # keys than a chunk (single-chunk passes).
+    ledger.ledger_reset()
+    stats = run_tensor_mode(ledger, num_kv=2, num_out=1, causal=causal, q_lengths=[2000, 1300, 500],
+                            k_lengths=[1800, 1200, 200], q_chunk=1536, kv_chunk=256, q_heads=8, kv_heads=2,
+                            head_dim=128, out_slots=False)
+    assert stats.d2h_bytes == 3800 * 8 * 128 * HEAD_BYTES
+    check(ledger, f"host_aliased d128 causal={causal}")
+
+
 def test_step_api_schedules_are_race_free(ledger):
     # The per-Q-block steps the Python executor drives for device consumers
     # and device outputs (seqattn/streaming/executor.py): output slots with

@@ -20,7 +20,7 @@ import pytest
 import torch
 
 from oracle.seqattn_oracle import chunked_attention
-from seqattn import StreamingAttentionConfig, StreamingAttentionRunner, build_plan
+from seqattn import StreamingAttentionConfig, StreamingAttentionRunner, StreamingAttentionStats, build_plan
 from seqattn.kernels import finalize_attention, update_attention_state
 
 pytestmark = pytest.mark.gpu
@@ -169,6 +169,40 @@ def test_host_aliased_and_device_resident_outputs_are_bit_identical_to_host_mode
     torch.testing.assert_close(device_out.cpu(), results[0][0], atol=0, rtol=0)
     ref_o, ref_l = oracle(q, k, v, cu, cu_k, q_chunk=256, kv_chunk=128, causal=False)
     check(results[0][0], results[0][1], ref_o, ref_l)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_host_aliased_piecewise_boundaries_are_bit_identical_to_host_mode(causal):
+    """host_aliased runs work each pass boundary in row pieces of the block
+    (the last chunk per piece, the output copied out and the next block's Q
+    rows copied in piece by piece, the first chunk per piece).  Blocks of 3-4
+    workgroup tiles give 3-4 pieces; the third segment has fewer keys than
+    one chunk, so its passes are a single (initializing, output-writing)
+    chunk; the second has fewer keys than queries, so under the causal rule
+    its first 100 rows see no key.  GQA 8/2, bf16."""
+    announce(f"host_aliased piecewise boundaries causal={causal}")
+    gen = torch.Generator().manual_seed(43)
+    cu_q = torch.tensor([0, 2000, 3300, 3800], dtype=torch.int32)
+    cu_k = torch.tensor([0, 1800, 3000, 3200], dtype=torch.int32)
+    q = pinned_randn((3800, 8, 128), torch.bfloat16, gen)
+    k = pinned_randn((3200, 2, 128), torch.bfloat16, gen)
+    v = pinned_randn((3200, 2, 128), torch.bfloat16, gen)
+    results = []
+    for mode in ("host", "host_aliased"):
+        config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=1536, kv_chunk_tokens=256, output_mode=mode)
+        stats = StreamingAttentionStats()
+        plan = build_plan(q_heads=8, kv_heads=2, head_dim=128, dtype=torch.bfloat16, device="cuda",
+                          max_q_tokens=3800, max_kv_tokens=3200, config=config)
+        runner = StreamingAttentionRunner(plan, config)
+        out, lse = runner(q, k, v, cu_q, cu_k, causal=causal, return_lse=True, stats=stats)
+        results.append((out, lse, stats))
+        runner.close()
+    (out_h, lse_h, st_h), (out_a, lse_a, st_a) = results
+    torch.testing.assert_close(out_a, out_h, atol=0, rtol=0)
+    torch.testing.assert_close(lse_a, lse_h, atol=0, rtol=0)
+    assert st_a.h2d_bytes == st_h.h2d_bytes and st_a.d2h_bytes == st_h.d2h_bytes == 3800 * 8 * 128 * 2
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=1536, kv_chunk=256, causal=causal)
+    check(out_a, lse_a, ref_o, ref_l)
 
 
 @pytest.mark.parametrize("kv_chunk", [96, 128])
