@@ -25,8 +25,9 @@ extern "C" {
 #endif
 
 /* 2: pipeline state in 16-row groups (sa_pipeline_create); fused finalize in
- * the pipeline's last chunk launches. */
-#define SA_ABI_VERSION 2
+ * the pipeline's last chunk launches.  3: head-group pipelines
+ * (sa_pipeline_create_head_groups). */
+#define SA_ABI_VERSION 3
 
 /* dtype codes for Q/K/V/output element types */
 #define SA_DTYPE_BF16 0
@@ -190,6 +191,45 @@ int32_t sa_pipeline_create(
     void* const* out_slots, int32_t num_output_buffers,
     int32_t q_chunk_tokens, int32_t kv_chunk_tokens,
     int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t dtype,
+    void* h2d_stream, void* d2h_stream);
+
+/*
+ * Bind a pipeline to the buffer sets of the head-group schedule.  No
+ * counterpart in the reference, whose resident Q super-block spans every head
+ * of a token range and streams all of K and V once per block (planner.py:187-325,
+ * streaming/executor.py:18-188).  Here a unit is every token of a group of
+ * group_kv_heads K/V heads and their q_heads / kv_heads query heads per K/V
+ * head, so each byte of Q, K and V crosses PCIe once per run.
+ *
+ *   qo_sets[i]   [max_q_tokens, group_kv_heads * (q_heads / kv_heads), head_dim] dtype:
+ *                a unit's Q columns, then its output
+ *   k_sets[i], v_sets[i]  [max_kv_tokens, group_kv_heads, head_dim] dtype
+ *   vt_sets      NULL, or num_sets device buffers of vt_bytes each: V of a
+ *                segment transposed per K/V head for head_dim 128, as for
+ *                sa_pipeline_attach_resident_scratch (used when a segment's
+ *                group_kv_heads * 128 * roundup(keys, 64) * 2 bytes fit)
+ *   num_sets     1 or 2; with 2, unit u uses set u % 2 and units alternate
+ *                between compute_stream and a second stream of the pipeline
+ *   kv_chunk_tokens  where the row sums merge, as in a token-block pipeline of
+ *                that K/V chunk, whose sa_pipeline_run output this matches bit
+ *                for bit; a segment longer than one chunk needs a chunk that is
+ *                a multiple of 64
+ *   h2d_stream, d2h_stream  as for sa_pipeline_create
+ * Buffers are contiguous and 16-byte aligned.  sa_pipeline_run on such a
+ * pipeline runs the head-group schedule: per unit, strided H2D copies of its
+ * Q, K and V columns of every token (after the set's previous output copy),
+ * one fused update launch per segment writing the output over the unit's Q
+ * rows and the LSE, and a strided D2H of the output columns.  Inputs may
+ * hold at most max_q_tokens / max_kv_tokens rows.  The step API
+ * (load_q ... d2h, attach_int8_scales) returns SA_ERR_BAD_STATE;
+ * sa_pipeline_run_resident works for segments its single fused launch
+ * covers.
+ */
+int32_t sa_pipeline_create_head_groups(
+    sa_pipeline** out_pipeline, int32_t device,
+    void* const* qo_sets, void* const* k_sets, void* const* v_sets, void* const* vt_sets, int64_t vt_bytes,
+    int32_t num_sets, int64_t max_q_tokens, int64_t max_kv_tokens, int32_t group_kv_heads,
+    int32_t kv_chunk_tokens, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t dtype,
     void* h2d_stream, void* d2h_stream);
 
 /* Wait for all pending copies of the pipeline, then release its events and the streams it created. */

@@ -164,6 +164,19 @@ struct sa_pipeline {
   bool out_pending[2] = {false, false};
   int64_t ring_next = 0;  // next K/V ring slot (rotates across calls)
 
+  // Head-group schedule (sa_pipeline_create_head_groups).  A unit is every
+  // token of a group of K/V heads and their query heads; each buffer set
+  // holds one unit's Q (then its output), K, V and optionally V transposed.
+  // Per set: ready (the unit's copies landed), done (its output written),
+  // free (its output copied out).
+  bool head_groups = false;
+  static constexpr int kMaxSets = 2;
+  int num_sets = 0, group_kv = 0;
+  int64_t hg_max_q = 0, hg_max_kv = 0, hg_vt_bytes = 0;
+  void* set_qo[kMaxSets] = {}, *set_k[kMaxSets] = {}, *set_v[kMaxSets] = {}, *set_vt[kMaxSets] = {};
+  hipEvent_t set_ready[kMaxSets] = {}, set_done[kMaxSets] = {}, set_free[kMaxSets] = {};
+  bool set_pending[kMaxSets] = {false, false};
+
   // Host-side trace ranges around each stage's enqueue (sa_pipeline_set_trace_ranges).
   bool trace = false;
   // Optional timing of update launches (event pairs on the compute stream).
@@ -208,6 +221,11 @@ void release(sa_pipeline* p) {
     if (p->piece_done[i]) (void)hipEventDestroy(p->piece_done[i]);
     if (p->piece_out[i]) (void)hipEventDestroy(p->piece_out[i]);
     if (p->piece_ready[i]) (void)hipEventDestroy(p->piece_ready[i]);
+  }
+  for (int i = 0; i < sa_pipeline::kMaxSets; ++i) {
+    if (p->set_ready[i]) (void)hipEventDestroy(p->set_ready[i]);
+    if (p->set_done[i]) (void)hipEventDestroy(p->set_done[i]);
+    if (p->set_free[i]) (void)hipEventDestroy(p->set_free[i]);
   }
   for (hipEvent_t e : p->t_start) (void)hipEventDestroy(e);
   for (hipEvent_t e : p->t_stop) (void)hipEventDestroy(e);
@@ -910,6 +928,184 @@ int32_t run_aliased(sa_pipeline* p, const char* qh, const char* kh, const char* 
   return 0;
 }
 
+// The step API works on a token-block pipeline's Q block, ring and state,
+// which a head-group pipeline does not have.
+int32_t require_token_blocks(const sa_pipeline* p, const char* what) {
+  if (!p->head_groups) return 0;
+  sa::set_error("%s: not available on a head-group pipeline (sa_pipeline_run runs its schedule)", what);
+  return SA_ERR_BAD_STATE;
+}
+
+// Copy `rows` rows of `width` bytes between buffers whose rows start `dpitch`
+// and `spitch` bytes apart: one flat copy when both sides are dense, else one
+// strided copy, which the copy engines run at the link's rate for rows of
+// 1 KB and more (about three quarters of it for 256-byte rows).
+int32_t copy_rows(void* dst, int64_t dpitch, const void* src, int64_t spitch, int64_t width, int64_t rows,
+                  hipMemcpyKind kind, hipStream_t stream) {
+  if (rows <= 0 || width <= 0) return 0;
+  if (dpitch == width && spitch == width) {
+    SA_HIP_RETURN(hipMemcpyAsync(dst, src, (size_t)(width * rows), kind, stream));
+  } else {
+    SA_HIP_RETURN(hipMemcpy2DAsync(dst, (size_t)dpitch, src, (size_t)spitch, (size_t)width, (size_t)rows, kind,
+                                   stream));
+  }
+  return 0;
+}
+
+// Merge interval of a fused launch over k_length keys: the plan's K/V chunk
+// (the row sums merge where the token-block schedule stores and reloads
+// them), or none when the chunk is not a multiple of the 64-key tile and the
+// whole span fits one chunk.  -1: the span cannot run as one fused launch.
+int32_t fused_merge_keys(const sa_pipeline* p, int64_t k_length) {
+  if (p->kv_chunk % 64 == 0) return p->kv_chunk;
+  return k_length <= p->kv_chunk ? 0 : -1;
+}
+
+// One fused update launch of the head-group schedule (initializes, runs over
+// every key of a segment, writes the output and the LSE), optionally
+// bracketed by timing events.
+int32_t launch_unit(sa_pipeline* p, const void* q, int64_t sq_t, const void* k, int64_t sk_t, const void* v,
+                    int64_t sv_t, int64_t sv_h, int32_t q_tokens, int32_t kv_tokens, int32_t q_heads,
+                    int32_t kv_heads, int32_t causal_shift, double scale, int32_t causal, int32_t merge_keys,
+                    const sa::FusedOutput& fused, bool v_transposed, hipStream_t stream) {
+  TraceRange range(p->trace, "seqattn:fused_update");
+  if (p->timing) {
+    if (p->t_used == p->t_start.size()) {
+      hipEvent_t a = nullptr, b = nullptr;
+      SA_HIP_RETURN(hipEventCreate(&a));
+      SA_HIP_RETURN(hipEventCreate(&b));
+      p->t_start.push_back(a);
+      p->t_stop.push_back(b);
+    }
+    SA_HIP_RETURN(hipEventRecord(p->t_start[p->t_used], stream));
+  }
+  const int32_t flags = (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE;
+  const int32_t rc = sa::launch_update(q, k, v, nullptr, nullptr, nullptr, sq_t, p->head_dim, sk_t, p->head_dim,
+                                       sv_t, sv_h, 0, 0, 0, 0, q_tokens, kv_tokens, q_heads, kv_heads, p->head_dim,
+                                       0, 0, causal_shift, scale, flags, p->dtype, stream, merge_keys, &fused,
+                                       v_transposed, /*tiled_state=*/false);
+  if (rc != 0) return rc;
+  if (p->timing) SA_HIP_RETURN(hipEventRecord(p->t_stop[p->t_used++], stream));
+  return 0;
+}
+
+// sa_pipeline_run on a head-group pipeline.  Unit u (K/V heads
+// [u * group_kv, ...), with their query heads) uses buffer set u % num_sets
+// and, with two sets, compute stream u % 2 (the caller's, then the
+// pipeline's second stream):
+//   H2D : [wait set_free] Q columns of every token, K and V columns (strided
+//         copies from the host's [token][head][d] rows), record set_ready;
+//   compute: wait set_ready; per segment [transpose V], one fused update
+//         launch over all its queries and keys that writes the output (over
+//         the unit's Q rows) and the LSE; record set_done;
+//   D2H : wait set_done; output columns back into the host rows, record
+//         set_free.
+// Every byte of Q, K and V crosses the link once.  The launch for unit u + 1
+// runs on the other stream, so it starts while unit u's last workgroups
+// drain, and its copies landed during unit u.  Each launch is the one
+// sa_pipeline_run_resident makes for those heads, which the per-chunk
+// schedule matches bit for bit.
+int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const char* vh, char* oh, float* lse,
+                        int64_t lse_sh, const int64_t* cu_q, const int64_t* cu_k, int32_t num_segments,
+                        double scale, int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
+  for (int32_t s = 0; s < num_segments; ++s) {
+    const int64_t q_length = cu_q[s + 1] - cu_q[s], k_length = cu_k[s + 1] - cu_k[s];
+    if (cu_q[s] < 0 || cu_k[s] < 0 || q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0) ||
+        cu_q[s + 1] > p->hg_max_q || cu_k[s + 1] > p->hg_max_kv || q_length > INT32_MAX || k_length > INT32_MAX) {
+      sa::set_error("sa_pipeline_run: segment %d has invalid bounds for this head-group pipeline", s);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    if (q_length > 0 && fused_merge_keys(p, k_length) < 0) {
+      sa::set_error("sa_pipeline_run: segment %d has %lld keys, more than one K/V chunk of %d, which is not a "
+                    "multiple of 64", s, (long long)k_length, p->kv_chunk);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+  }
+  if (num_segments <= 0) return 0;
+  const int64_t total_q = cu_q[num_segments], total_k = cu_k[num_segments];
+  const int group = p->q_heads / p->kv_heads;
+  const int64_t d_bytes = (int64_t)p->head_dim * 2;
+  const int64_t q_pitch = p->q_heads * d_bytes, kv_pitch = p->kv_heads * d_bytes;
+  const int units = (p->kv_heads + p->group_kv - 1) / p->group_kv;
+  hipStream_t streams[sa_pipeline::kMaxSets] = {compute, p->side};
+  SideJoin join{p, compute};
+  if (p->num_sets > 1 && units > 1) {
+    // The second stream starts after the caller's earlier work.
+    SA_HIP_RETURN(hipEventRecord(p->fork, compute));
+    SA_HIP_RETURN(hipStreamWaitEvent(p->side, p->fork, 0));
+    join.active = true;
+  }
+  for (int u = 0; u < units; ++u) {
+    const int b = u % p->num_sets;
+    hipStream_t cs = streams[b];
+    const int kv0 = u * p->group_kv;
+    const int gk = std::min(p->group_kv, p->kv_heads - kv0);
+    const int gq = gk * group;
+    const int64_t wq = gq * d_bytes, wk = gk * d_bytes;
+    char* qo = static_cast<char*>(p->set_qo[b]);
+    char* kd = static_cast<char*>(p->set_k[b]);
+    char* vd = static_cast<char*>(p->set_v[b]);
+    {
+      TraceRange range(p->trace, "seqattn:q_h2d");
+      if (p->set_pending[b]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->set_free[b], 0));
+      int32_t rc = copy_rows(qo, wq, qh + (int64_t)kv0 * group * d_bytes, q_pitch, wq, total_q,
+                             hipMemcpyHostToDevice, p->h2d);
+      if (rc != 0) return rc;
+    }
+    {
+      TraceRange range(p->trace, "seqattn:kv_h2d");
+      int32_t rc = copy_rows(kd, wk, kh + kv0 * d_bytes, kv_pitch, wk, total_k, hipMemcpyHostToDevice, p->h2d);
+      if (rc == 0) rc = copy_rows(vd, wk, vh + kv0 * d_bytes, kv_pitch, wk, total_k, hipMemcpyHostToDevice, p->h2d);
+      if (rc != 0) return rc;
+      SA_HIP_RETURN(hipEventRecord(p->set_ready[b], p->h2d));
+    }
+    add_stats(st, total_q * wq + 2 * total_k * wk, 0, 1, 0, total_q);
+    SA_HIP_RETURN(hipStreamWaitEvent(cs, p->set_ready[b], 0));
+    int64_t chunks = 0;
+    for (int32_t s = 0; s < num_segments; ++s) {
+      const int64_t q_start = cu_q[s], k_start = cu_k[s];
+      const int64_t q_length = cu_q[s + 1] - q_start, k_length = cu_k[s + 1] - k_start;
+      if (q_length == 0) continue;
+      const int64_t t_pad = (k_length + 63) / 64 * 64;
+      const bool vt = p->head_dim == 128 && p->set_vt[b] != nullptr && gk * 128 * t_pad * 2 <= p->hg_vt_bytes &&
+                      t_pad < (1 << 24);
+      const char* vseg = vd + k_start * wk;
+      if (vt) {
+        const int32_t rc = sa::launch_transpose_v(vseg, gk * p->head_dim, p->head_dim, (int32_t)k_length, gk,
+                                                  p->head_dim, p->set_vt[b], t_pad, cs);
+        if (rc != 0) return rc;
+      }
+      const sa::FusedOutput fused{qo + q_start * wq, (int64_t)gq * p->head_dim, p->head_dim,
+                                  lse ? lse + (int64_t)kv0 * group * lse_sh : nullptr, lse_sh, q_start};
+      const int32_t rc = launch_unit(p, qo + q_start * wq, (int64_t)gq * p->head_dim, kd + k_start * wk,
+                                     (int64_t)gk * p->head_dim, vt ? static_cast<const char*>(p->set_vt[b]) : vseg,
+                                     vt ? t_pad : (int64_t)gk * p->head_dim, vt ? 128 * t_pad : p->head_dim,
+                                     (int32_t)q_length, (int32_t)k_length, gq, gk, (int32_t)(k_length - q_length),
+                                     scale, causal, fused_merge_keys(p, k_length), fused, vt, cs);
+      if (rc != 0) return rc;
+      chunks += (k_length + p->kv_chunk - 1) / p->kv_chunk;
+    }
+    add_stats(st, 0, 0, 0, chunks, 0);
+    SA_HIP_RETURN(hipEventRecord(p->set_done[b], cs));
+    {
+      TraceRange range(p->trace, "seqattn:output_d2h");
+      SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->set_done[b], 0));
+      const int32_t rc = copy_rows(oh + (int64_t)kv0 * group * d_bytes, q_pitch, qo, wq, wq, total_q,
+                                   hipMemcpyDeviceToHost, p->d2h);
+      if (rc != 0) return rc;
+      SA_HIP_RETURN(hipEventRecord(p->set_free[b], p->d2h));
+      p->set_pending[b] = true;
+    }
+    add_stats(st, 0, total_q * wq, 0, 0, 0);
+  }
+  // Work the caller enqueues on compute_stream later (a read of the LSE)
+  // follows the second stream's launches.
+  const int32_t jrc = join.finish();
+  if (jrc != 0) return jrc;
+  SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -1043,6 +1239,108 @@ int32_t sa_pipeline_create(sa_pipeline** out_pipeline, int32_t device, void* q_b
   return 0;
 }
 
+int32_t sa_pipeline_create_head_groups(sa_pipeline** out_pipeline, int32_t device, void* const* qo_sets,
+                                       void* const* k_sets, void* const* v_sets, void* const* vt_sets,
+                                       int64_t vt_bytes, int32_t num_sets, int64_t max_q_tokens,
+                                       int64_t max_kv_tokens, int32_t group_kv_heads, int32_t kv_chunk_tokens,
+                                       int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t dtype,
+                                       void* h2d_stream, void* d2h_stream) {
+  sa::clear_error();
+  if (!out_pipeline) {
+    sa::set_error("sa_pipeline_create_head_groups: null out_pipeline");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  *out_pipeline = nullptr;
+  if (num_sets < 1 || num_sets > sa_pipeline::kMaxSets || max_q_tokens < 0 || max_kv_tokens < 0 ||
+      kv_chunk_tokens <= 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads != 0 || group_kv_heads <= 0 ||
+      group_kv_heads > kv_heads || head_dim <= 0 || head_dim % 8 != 0 || vt_bytes < 0) {
+    sa::set_error("sa_pipeline_create_head_groups: invalid plan (sets %d, tokens %lld/%lld, kv_chunk %d, heads "
+                  "%d/%d, %d K/V heads per group, head_dim %d)",
+                  num_sets, (long long)max_q_tokens, (long long)max_kv_tokens, kv_chunk_tokens, q_heads, kv_heads,
+                  group_kv_heads, head_dim);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (dtype != SA_DTYPE_BF16 && dtype != SA_DTYPE_FP16) {
+    sa::set_error("sa_pipeline_create_head_groups: unsupported dtype code %d", dtype);
+    return SA_ERR_UNSUPPORTED_DTYPE;
+  }
+  if (!qo_sets || !k_sets || !v_sets) {
+    sa::set_error("sa_pipeline_create_head_groups: null buffer set array");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  for (int i = 0; i < num_sets; ++i) {
+    const uintptr_t bits = reinterpret_cast<uintptr_t>(qo_sets[i]) | reinterpret_cast<uintptr_t>(k_sets[i]) |
+                           reinterpret_cast<uintptr_t>(v_sets[i]) |
+                           (vt_sets ? reinterpret_cast<uintptr_t>(vt_sets[i]) : 0);
+    if (!qo_sets[i] || !k_sets[i] || !v_sets[i] || (vt_sets && vt_bytes > 0 && !vt_sets[i]) || bits % 16 != 0) {
+      sa::set_error("sa_pipeline_create_head_groups: buffer set %d has a null or misaligned buffer", i);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+  }
+  sa_pipeline* p = new (std::nothrow) sa_pipeline();
+  if (!p) {
+    sa::set_error("sa_pipeline_create_head_groups: out of host memory");
+    return SA_ERR_BAD_STATE;
+  }
+  p->device = device;
+  p->head_groups = true;
+  p->num_sets = num_sets;
+  p->group_kv = group_kv_heads;
+  p->hg_max_q = max_q_tokens;
+  p->hg_max_kv = max_kv_tokens;
+  p->hg_vt_bytes = vt_sets ? vt_bytes : 0;
+  for (int i = 0; i < num_sets; ++i) {
+    p->set_qo[i] = qo_sets[i];
+    p->set_k[i] = k_sets[i];
+    p->set_v[i] = v_sets[i];
+    p->set_vt[i] = vt_sets && vt_bytes > 0 ? vt_sets[i] : nullptr;
+  }
+  p->kv_chunk = kv_chunk_tokens;
+  p->q_heads = q_heads;
+  p->kv_heads = kv_heads;
+  p->head_dim = head_dim;
+  p->dtype = dtype;
+  p->q_row_bytes = (int64_t)q_heads * head_dim * 2;
+  p->kv_row_bytes = (int64_t)kv_heads * head_dim * 2;
+
+  sa::DeviceGuard guard(device);
+  hipError_t err = guard.status();
+  if (err != hipSuccess) {
+    delete p;
+    return sa::hip_status(err, "sa_pipeline_create_head_groups: selecting the device");
+  }
+  if ((h2d_stream == nullptr) != (d2h_stream == nullptr)) {
+    delete p;
+    sa::set_error("sa_pipeline_create_head_groups: pass both copy streams or neither");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (h2d_stream) {
+    p->h2d = static_cast<hipStream_t>(h2d_stream);
+    p->d2h = static_cast<hipStream_t>(d2h_stream);
+  } else {
+    p->owns_streams = true;
+    err = hipStreamCreateWithFlags(&p->h2d, hipStreamNonBlocking);
+    if (err == hipSuccess) err = hipStreamCreateWithFlags(&p->d2h, hipStreamNonBlocking);
+  }
+  const unsigned flags = hipEventDisableTiming;
+  if (err == hipSuccess) err = hipStreamCreateWithFlags(&p->side, hipStreamNonBlocking);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&p->fork, flags);
+  if (err == hipSuccess) err = hipEventCreateWithFlags(&p->join, flags);
+  for (int i = 0; i < num_sets && err == hipSuccess; ++i) {
+    err = hipEventCreateWithFlags(&p->set_ready[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->set_done[i], flags);
+    if (err == hipSuccess) err = hipEventCreateWithFlags(&p->set_free[i], flags);
+  }
+  if (err != hipSuccess) {
+    int32_t rc = sa::hip_status(err, "sa_pipeline_create_head_groups stream/event creation");
+    release(p);
+    delete p;
+    return rc;
+  }
+  *out_pipeline = p;
+  return 0;
+}
+
 int32_t sa_pipeline_destroy(sa_pipeline* p) {
   sa::clear_error();
   if (!p) return 0;
@@ -1058,6 +1356,7 @@ int32_t sa_pipeline_load_q(sa_pipeline* p, const void* q_host, int32_t q_tokens,
                            void* compute_stream, sa_pipeline_stats* stats) {
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_load_q")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   return load_q(p, q_host, q_tokens, static_cast<hipStream_t>(compute_stream), stats);
@@ -1069,6 +1368,7 @@ int32_t sa_pipeline_stream_kv(sa_pipeline* p, const void* k_host, const void* v_
                               void* compute_stream, sa_pipeline_stats* stats) {
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_stream_kv")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   return stream_kv(p, k_host, v_host, k_length, q_tokens, q_local_offset, causal_shift,
@@ -1086,6 +1386,7 @@ int32_t sa_pipeline_stream_kv_span(sa_pipeline* p, const void* k_host, const voi
     sa::set_error("sa_pipeline_stream_kv_span: null argument");
     return SA_ERR_INVALID_ARGUMENT;
   }
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_stream_kv_span")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
@@ -1119,6 +1420,7 @@ int32_t sa_pipeline_stream_kv_gather(sa_pipeline* p, const void* const* k_fragme
     sa::set_error("sa_pipeline_stream_kv_gather: null argument");
     return SA_ERR_INVALID_ARGUMENT;
   }
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_stream_kv_gather")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
@@ -1138,6 +1440,7 @@ int32_t sa_pipeline_attach_int8_scales(sa_pipeline* p, void* const* k_scale_slot
                   p ? p->num_kv : 0);
     return SA_ERR_INVALID_ARGUMENT;
   }
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_attach_int8_scales")) return hg;
   if (p->head_dim % 16 != 0 || p->head_dim > 128) {
     sa::set_error("sa_pipeline_attach_int8_scales: INT8 K/V needs head_dim a multiple of 16 up to "
                   "128, got %d", p->head_dim);
@@ -1171,6 +1474,7 @@ int32_t sa_pipeline_stream_kv_gather_int8(
     sa::set_error("sa_pipeline_stream_kv_gather_int8: null argument");
     return SA_ERR_INVALID_ARGUMENT;
   }
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_stream_kv_gather_int8")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
@@ -1218,8 +1522,19 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
     KVSource src{kd + k_start * stride_kt * 2, vd + k_start * stride_vt * 2, true,
                  stride_kt, stride_kh, stride_vt, stride_vh};
     char* seg_out = od + q_start * stride_ot * 2;
-    if (q_length > 0 && p->kv_chunk % 64 == 0 && q_length <= INT32_MAX && k_length <= INT32_MAX &&
-        stride_ot % 8 == 0 && stride_oh % 8 == 0 && reinterpret_cast<uintptr_t>(seg_out) % 16 == 0) {
+    // A head-group pipeline has no Q block or state buffers: only the single
+    // fused launch below is available to it.
+    const int32_t merge = p->head_groups ? fused_merge_keys(p, k_length) : (p->kv_chunk % 64 == 0 ? p->kv_chunk : -1);
+    const bool fused_segment = q_length > 0 && merge >= 0 && q_length <= INT32_MAX && k_length <= INT32_MAX &&
+                               stride_ot % 8 == 0 && stride_oh % 8 == 0 &&
+                               reinterpret_cast<uintptr_t>(seg_out) % 16 == 0;
+    if (p->head_groups && q_length > 0 && !fused_segment) {
+      sa::set_error("sa_pipeline_run_resident: segment %d needs the chunked schedule (a 16-byte aligned output "
+                    "with strides that are multiples of 8, and at most one K/V chunk unless the chunk is a "
+                    "multiple of 64), which a head-group pipeline does not have", s);
+      return SA_ERR_BAD_STATE;
+    }
+    if (fused_segment) {
       // K/V already in HBM: one launch covers every query and key of the
       // segment and finalizes its rows in the epilogue.  The row sums are
       // merged at every kv_chunk boundary exactly as the chunked schedule
@@ -1244,10 +1559,11 @@ int32_t sa_pipeline_run_resident(sa_pipeline* p, const void* q, const void* k, c
       rc = launch_timed(p, qd + q_start * stride_qt * 2, stride_qt, stride_qh, src.k, src.sk_t, src.sk_h,
                         vt ? static_cast<const char*>(p->vt_scratch) : src.v, vt ? t_pad : src.sv_t,
                         vt ? 128 * t_pad : src.sv_h, (int32_t)q_length, (int32_t)k_length, 0, 0, causal_shift,
-                        softmax_scale, (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, p->kv_chunk,
+                        softmax_scale, (causal ? SA_FLAG_CAUSAL : 0) | SA_FLAG_INITIALIZE, compute, merge,
                         &fused, 0, vt);
       if (rc != 0) return rc;
-      const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
+      const int64_t block = p->head_groups ? q_length
+                                           : pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
       for (int64_t qs = q_start; qs < q_stop; qs += block) {
         const int64_t n = std::min<int64_t>(block, q_stop - qs);
         const int64_t visible_end = causal ? std::max<int64_t>(0, qs - q_start + n + causal_shift) : INT64_MAX;
@@ -1286,6 +1602,7 @@ int32_t sa_pipeline_finalize(sa_pipeline* p, int32_t slot, int32_t q_tokens, flo
                              int64_t lse_stride_h, int64_t lse_token_offset, void* compute_stream) {
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_finalize")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   return finalize(p, slot, q_tokens, lse, lse_stride_h, lse_token_offset,
@@ -1302,6 +1619,7 @@ int32_t sa_pipeline_finalize_into(sa_pipeline* p, void* dest, int64_t stride_ot,
     sa::set_error("q_tokens %d outside [0, q_chunk_tokens=%d]", q_tokens, p->q_chunk);
     return SA_ERR_INVALID_ARGUMENT;
   }
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_finalize_into")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   hipStream_t compute = static_cast<hipStream_t>(compute_stream);
@@ -1317,6 +1635,7 @@ int32_t sa_pipeline_finalize_into(sa_pipeline* p, void* dest, int64_t stride_ot,
 int32_t sa_pipeline_release_q(sa_pipeline* p, void* compute_stream) {
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_release_q")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   SA_HIP_RETURN(hipEventRecord(p->q_free, static_cast<hipStream_t>(compute_stream)));
@@ -1329,6 +1648,7 @@ int32_t sa_pipeline_d2h(sa_pipeline* p, void* dst_host, const void* src, int64_t
                         sa_pipeline_stats* stats) {
   sa::clear_error();
   if (!p) return SA_ERR_INVALID_ARGUMENT;
+  if (const int32_t hg = require_token_blocks(p, "sa_pipeline_d2h")) return hg;
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
   return d2h(p, dst_host, src, bytes, event_slot, release_q,
@@ -1447,6 +1767,9 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
   const char* kh = static_cast<const char*>(k_host);
   const char* vh = static_cast<const char*>(v_host);
   char* oh = static_cast<char*>(out_host);
+  if (p->head_groups)
+    return run_head_groups(p, qh, kh, vh, oh, lse, lse_stride_h, cu_seqlens_q, cu_seqlens_k, num_segments,
+                           softmax_scale, causal, compute, stats);
   if (!p->has_out_slots || p->num_out == 1) {
     std::vector<Pass> passes;
     for (int32_t s = 0; s < num_segments; ++s) {

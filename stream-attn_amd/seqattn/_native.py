@@ -16,7 +16,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads the HIP runtime the library binds to)
 
 LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libseqattn_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 SA_DTYPE_BF16 = 0
 SA_DTYPE_FP16 = 1
@@ -67,6 +67,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [ctypes.POINTER(c_void_p), c_int32, c_void_p, ctypes.POINTER(c_void_p),
          ctypes.POINTER(c_void_p), c_int32, c_void_p, c_void_p, c_void_p,
          ctypes.POINTER(c_void_p), c_int32] + [c_int32] * 6 + [c_void_p, c_void_p],
+    ),
+    "sa_pipeline_create_head_groups": (
+        c_int32,
+        [ctypes.POINTER(c_void_p), c_int32] + [ctypes.POINTER(c_void_p)] * 4 + [c_int64, c_int32, c_int64, c_int64]
+        + [c_int32] * 6 + [c_void_p, c_void_p],
     ),
     "sa_pipeline_destroy": (c_int32, [c_void_p]),
     "sa_pipeline_run": (

@@ -10,6 +10,14 @@ and configuration files carry over unchanged.  Differences:
   finalized into the resident Q buffer and copied back from there, which frees
   the raw output slots from the HBM budget (a larger resident Q block and
   fewer passes over K/V).
+* ``schedule`` selects how the workspace is filled.  ``"q_blocks"`` (the
+  default) is the reference's schedule: a resident Q super-block spans every
+  head of a token range and all of K/V streams through the ring once per
+  block.  ``"head_groups"`` keeps every token of a group of K/V heads (with
+  their query heads) in HBM at once, so each byte of Q, K and V crosses PCIe
+  once per run; it returns the output to host memory (``output_mode``
+  ``"host"`` or ``"host_aliased"``), and its results equal the default
+  schedule's bit for bit.
 """
 
 from __future__ import annotations
@@ -18,6 +26,7 @@ from dataclasses import dataclass, field
 
 BACKENDS = {"auto", "hip", "triton", "reference"}
 OUTPUT_MODES = {"host", "host_aliased", "device_consumer"}
+SCHEDULES = {"q_blocks", "head_groups"}
 
 
 @dataclass(frozen=True)
@@ -56,6 +65,10 @@ class StreamingAttentionConfig:
     # scratch the runner may allocate.  Without it V is read in place, with
     # bit-identical results.
     resident_scratch_limit_bytes: int | None = None
+    # "q_blocks": the reference's Q super-block schedule.  "head_groups":
+    # every token of a group of K/V heads resident at once (Q, K and V cross
+    # PCIe once; host output only).
+    schedule: str = "q_blocks"
 
     def validate(self) -> None:
         if self.workspace_budget_bytes is not None and self.workspace_budget_bytes <= 0:
@@ -82,6 +95,11 @@ class StreamingAttentionConfig:
             raise ValueError("num_stages must be within [1, 4]")
         if self.backend not in BACKENDS:
             raise ValueError(f"unsupported backend: {self.backend}")
+        if self.schedule not in SCHEDULES:
+            raise ValueError("schedule must be 'q_blocks' or 'head_groups'")
+        if self.schedule == "head_groups" and self.output_mode == "device_consumer":
+            raise ValueError("schedule='head_groups' returns the output to host memory; "
+                             "device_consumer output needs schedule='q_blocks'")
 
 
 @dataclass(frozen=True)
@@ -187,5 +205,6 @@ __all__ = [
     "PagedAttentionConfig",
     "ProjectionPipelineConfig",
     "QKV_RESIDENCIES",
+    "SCHEDULES",
     "StreamingAttentionConfig",
 ]

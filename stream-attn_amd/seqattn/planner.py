@@ -29,6 +29,15 @@ every head_dim: Q chunks align to 128 rows and K/V chunks to the kernel's
 for head_dim <= 64, and the last workgroup of a chunk is masked, so 128-row
 alignment costs at most one partly masked workgroup per chunk).  ``output_mode="host_aliased"`` charges no raw
 output slots because the output is finalized into the Q buffer.
+
+Head-group schedule (``config.schedule == "head_groups"``, an addition): the
+workspace holds one or two buffer sets, each with every query and key token
+of a group of K/V heads (Q, then the output over it; K; V; and V transposed
+for head_dim 128).  The planner picks two sets when one K/V head fits twice
+(copies of the next unit overlap the current unit's launches), then the
+largest group of K/V heads the budget allows, evened out over the units.  The
+plan's K/V chunk is the one the default schedule picks for the same budget:
+the row sums merge there, so both schedules give the same bits.
 """
 
 from __future__ import annotations
@@ -123,6 +132,12 @@ class AttentionPlan:
     # max_kv_tokens, and the share of the measured H2D rate it keeps busy.
     estimated_seconds: float | None = None
     h2d_link_fraction: float | None = None
+    # "q_blocks" or "head_groups"; for head groups, the K/V heads per unit,
+    # the buffer sets and each set's transposed-V bytes (0: V read in place).
+    schedule: str = "q_blocks"
+    head_group_kv_heads: int = 0
+    head_group_sets: int = 0
+    head_group_vt_bytes: int = 0
 
     @property
     def group_size(self) -> int:
@@ -130,8 +145,14 @@ class AttentionPlan:
 
     @property
     def q_passes(self) -> int:
-        """Passes over K/V for one segment of max_q_tokens queries."""
+        """Passes over K/V for one segment of max_q_tokens queries (one for
+        head groups: each unit reads its heads' K/V once)."""
         return math.ceil(self.max_q_tokens / self.q_chunk_tokens)
+
+    @property
+    def head_group_units(self) -> int:
+        """Units of the head-group schedule (0 for the Q-block schedule)."""
+        return math.ceil(self.kv_heads / self.head_group_kv_heads) if self.head_group_kv_heads else 0
 
 
 def estimate_workspace_bytes(
@@ -259,6 +280,55 @@ def modeled_run(
     return seconds, passes * h2d_pass / seconds
 
 
+def head_group_set_bytes(*, group_kv_heads: int, max_q_tokens: int, max_kv_tokens: int, q_heads: int,
+                         kv_heads: int, head_dim: int, dtype: torch.dtype, transposed_v: bool) -> int:
+    """Bytes of one head-group buffer set: Q/output, K, V and optionally V
+    transposed ([heads][128][keys rounded up to 64], head_dim 128 only)."""
+    element = _element_size(dtype)
+    group = q_heads // kv_heads
+    per_head = max_q_tokens * group * head_dim * element + 2 * max_kv_tokens * head_dim * element
+    if transposed_v:
+        per_head += 128 * ((max_kv_tokens + 63) // 64 * 64) * 2
+    return group_kv_heads * per_head
+
+
+def _head_group_layout(*, budget: int | None, max_q_tokens: int, max_kv_tokens: int, q_heads: int, kv_heads: int,
+                       head_dim: int, dtype: torch.dtype) -> tuple[int, int, bool] | None:
+    """(sets, K/V heads per unit, transposed V) for the budget, or None."""
+    options = (True, False) if head_dim == 128 else (False,)
+    for sets in (2, 1):
+        for transposed_v in options:
+            per_head = head_group_set_bytes(group_kv_heads=1, max_q_tokens=max_q_tokens, max_kv_tokens=max_kv_tokens,
+                                            q_heads=q_heads, kv_heads=kv_heads, head_dim=head_dim, dtype=dtype,
+                                            transposed_v=transposed_v)
+            if budget is None:
+                fit = kv_heads
+            else:
+                fit = min(kv_heads, max(budget - FIXED_MARGIN_BYTES, 0) // (sets * per_head))
+            if fit >= 1:
+                units = math.ceil(kv_heads / fit)
+                return sets, math.ceil(kv_heads / units), transposed_v
+    return None
+
+
+def modeled_head_groups(*, max_q_tokens: int, max_kv_tokens: int, q_heads: int, kv_heads: int, head_dim: int,
+                        dtype: torch.dtype, group_kv_heads: int, sets: int, rates: PlannerRates) -> tuple[float, float]:
+    """(seconds, H2D link fraction) of one non-causal head-group run: every
+    unit's launches at the measured rate; with two sets only the first unit's
+    copies and the last unit's output copy are exposed, with one set every
+    unit's copies are."""
+    element = _element_size(dtype)
+    units = math.ceil(kv_heads / group_kv_heads)
+    h2d = (max_q_tokens * q_heads + 2 * max_kv_tokens * kv_heads) * head_dim * element
+    d2h = max_q_tokens * q_heads * head_dim * element
+    kernel = 4.0 * q_heads * head_dim * max_q_tokens * max_kv_tokens / rates.update_flops_per_second
+    copy_in = h2d / rates.h2d_bytes_per_second
+    copy_out = d2h / rates.h2d_bytes_per_second
+    exposed = (copy_in + copy_out) / units if sets > 1 else copy_in + copy_out
+    seconds = kernel + exposed + units * rates.launch_seconds
+    return seconds, copy_in / seconds
+
+
 def measure_planner_rates(device: torch.device | str = "cuda", *, dtype: torch.dtype = torch.bfloat16,
                           copy_bytes: int = 512 * 2**20) -> PlannerRates:
     """Measure the pinned H2D copy rate and the update kernel's rate on
@@ -317,7 +387,9 @@ def build_plan(
 
     ``rates`` (optional): measured device rates; the candidates are then
     ranked by the modeled run time of this pipeline instead of the
-    reference's fixed-constant cost."""
+    reference's fixed-constant cost.  With ``config.schedule ==
+    "head_groups"`` the plan sizes head-group buffer sets instead (module
+    docstring)."""
     config = StreamingAttentionConfig() if config is None else config
     config.validate()
     device = torch.device(device)
@@ -363,6 +435,16 @@ def build_plan(
             cost = modeled_run(**sizes, rates=rates, **shape)[0]
         scored.append((cost, q_chunk, kv_chunk))
 
+    if config.schedule == "head_groups":
+        # The default schedule's K/V chunk for the same inputs (row sums merge
+        # there), rounded to whole 64-key tiles when a segment can be longer.
+        if scored:
+            kv_chunk = min(scored)[2]
+        else:
+            kv_chunk = min(max(config.block_n, _align_down(min(kv_options), config.block_n)), max_kv_tokens)
+        if kv_chunk % 64 and kv_chunk < max_kv_tokens:
+            kv_chunk = max(64, _align_down(kv_chunk, 64))
+        return _build_head_group_plan(kv_chunk, config, device, max_q_tokens, max_kv_tokens, shape, rates)
     if not scored:
         smallest = _workspace_for(min(config.block_m, max_q_tokens), min(kv_options), shape, config)
         raise ValueError(
@@ -382,7 +464,7 @@ def build_plan(
     if rates is not None:
         modeled = modeled_run(q_chunk=q_chunk, kv_chunk=kv_chunk, max_q_tokens=max_q_tokens,
                               max_kv_tokens=max_kv_tokens, rates=rates, **shape)
-    return AttentionPlan(
+    plan = AttentionPlan(
         q_heads=q_heads,
         kv_heads=kv_heads,
         head_dim=head_dim,
@@ -404,6 +486,57 @@ def build_plan(
         estimated_seconds=modeled[0],
         h2d_link_fraction=modeled[1],
     )
+    return plan
+
+
+def _build_head_group_plan(kv_chunk: int, config: StreamingAttentionConfig, device: torch.device,
+                           max_q_tokens: int, max_kv_tokens: int, shape: dict,
+                           rates: PlannerRates | None) -> AttentionPlan:
+    """The head-group plan for a shape and budget, merging row sums every
+    ``kv_chunk`` keys."""
+    budget = config.workspace_budget_bytes
+    layout = _head_group_layout(budget=budget, max_q_tokens=max_q_tokens, max_kv_tokens=max_kv_tokens, **shape)
+    if layout is None:
+        need = 1 * head_group_set_bytes(group_kv_heads=1, max_q_tokens=max_q_tokens, max_kv_tokens=max_kv_tokens,
+                                        transposed_v=False, **shape) + FIXED_MARGIN_BYTES
+        raise ValueError(
+            "workspace budget is too small for the head-group schedule (every token of one K/V head): "
+            f"need at least {need / 2**20:.1f} MiB"
+        )
+    sets, group_kv, transposed_v = layout
+    set_bytes = head_group_set_bytes(group_kv_heads=group_kv, max_q_tokens=max_q_tokens,
+                                     max_kv_tokens=max_kv_tokens, transposed_v=transposed_v, **shape)
+    vt_bytes = group_kv * 128 * ((max_kv_tokens + 63) // 64 * 64) * 2 if transposed_v else 0
+    modeled = (None, None)
+    if rates is not None:
+        modeled = modeled_head_groups(max_q_tokens=max_q_tokens, max_kv_tokens=max_kv_tokens, group_kv_heads=group_kv,
+                                      sets=sets, rates=rates, **shape)
+    return AttentionPlan(
+        q_heads=shape["q_heads"],
+        kv_heads=shape["kv_heads"],
+        head_dim=shape["head_dim"],
+        dtype=shape["dtype"],
+        device=device,
+        max_q_tokens=max_q_tokens,
+        max_kv_tokens=max_kv_tokens,
+        q_chunk_tokens=max_q_tokens,
+        kv_chunk_tokens=kv_chunk,
+        num_kv_buffers=config.num_kv_buffers,
+        num_output_buffers=config.num_output_buffers,
+        output_mode=config.output_mode,
+        block_m=config.block_m,
+        block_n=config.block_n,
+        num_warps=config.num_warps,
+        num_stages=config.num_stages,
+        estimated_workspace_bytes=sets * set_bytes + FIXED_MARGIN_BYTES,
+        workspace_budget_bytes=budget,
+        estimated_seconds=modeled[0],
+        h2d_link_fraction=modeled[1],
+        schedule="head_groups",
+        head_group_kv_heads=group_kv,
+        head_group_sets=sets,
+        head_group_vt_bytes=vt_bytes,
+    )
 
 
 __all__ = [
@@ -411,6 +544,8 @@ __all__ = [
     "PlannerRates",
     "build_plan",
     "estimate_workspace_bytes",
+    "head_group_set_bytes",
     "measure_planner_rates",
+    "modeled_head_groups",
     "modeled_run",
 ]

@@ -54,6 +54,8 @@ class ProjectedAttentionRunner:
         self.pipeline_config = ProjectionPipelineConfig() if pipeline_config is None else pipeline_config
         self.attention_config.validate()
         self.pipeline_config.validate()
+        if self.attention_config.schedule != "q_blocks":
+            raise ValueError("the projected pipeline projects each finished Q tile: it needs schedule='q_blocks'")
         # The plan is rebuilt against the runner's own attention config, as
         # the reference does, so a plan made with other launch settings
         # still gets a consistent workspace.

@@ -11,6 +11,10 @@ signatures and validation as the reference.  Additive options:
 * q, k and v may be device tensors on the plan's device (HBM-resident
   inputs): the same Q super-block / K/V chunk schedule then reads them in
   place, nothing crosses PCIe and the output is a device tensor.
+* A plan of the head-group schedule (``schedule="head_groups"``) runs host
+  inputs into a host ``out`` with one native call per run, each byte of Q,
+  K and V crossing PCIe once; device outputs and ``run_with_device_output``
+  need the default schedule.
 """
 
 from __future__ import annotations
@@ -139,6 +143,9 @@ class StreamingAttentionRunner(HipExecutorMixin):
         if out.shape != q_cpu.shape or out.dtype != q_cpu.dtype or out.device.type not in {"cpu", "cuda"}:
             raise ValueError("out must be a CPU tensor matching q shape and dtype")
         self._prepare_io(q_cpu, k_cpu, v_cpu, out)
+        if out.device.type != "cpu" and self.plan.schedule == "head_groups":
+            raise ValueError("schedule='head_groups' returns the output to host memory; "
+                             "a device out needs schedule='q_blocks'")
         lse = self._lse_buffer(q_cpu.shape[0], lse_out, return_lse)
         stats = self._prepare_stats(stats)
         started = time.perf_counter()
@@ -192,6 +199,9 @@ class StreamingAttentionRunner(HipExecutorMixin):
         """
         if q_cpu.device.type != "cpu":
             raise ValueError("seqattn expects CPU-backed q, k, and v tensors")
+        if self.plan.schedule == "head_groups":
+            raise ValueError("run_with_device_output needs schedule='q_blocks' (head groups finish every "
+                             "query row of a head group at once, not tile by tile)")
         q_bounds, k_bounds = self._validate_inputs(q_cpu, k_cpu, v_cpu, cu_seqlens_q, cu_seqlens_k)
         if out.device.type not in {"cpu", "cuda"} or out.shape[0] != q_cpu.shape[0]:
             raise ValueError("out must be a CPU tensor with one row per query token")

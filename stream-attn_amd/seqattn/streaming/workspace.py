@@ -8,6 +8,11 @@ They are torch allocations, so the planner's budget accounts for all of them.
 The ready/free events live in the native pipeline object bound to these
 buffers; copies run on two torch streams handed to it and compute on torch's
 current stream at creation.
+
+A plan of the head-group schedule allocates its buffer sets instead: per set,
+Q/output ``[max_q_tokens, Hq_group, D]``, K and V ``[max_kv_tokens,
+Hkv_group, D]`` and, for head_dim 128, the transposed-V scratch of one
+segment.  It has no Q block, ring or state buffers.
 """
 
 from __future__ import annotations
@@ -70,6 +75,58 @@ class CudaWorkspace:
     def __init__(self, plan: AttentionPlan) -> None:
         device = plan.device
         self.device = device
+        self.compute_stream = torch.cuda.current_stream(device)
+        # Copy streams are torch streams (default priority) so torch's caching
+        # allocator can track their uses of workspace and consumer buffers
+        # (record_stream) for as long as those buffers live.
+        self.h2d_stream, self.d2h_stream = copy_streams(device)
+        self._lib = _native.lib()
+        self.plan = plan
+        self.resident_scratch: torch.Tensor | None = None
+        if plan.schedule == "head_groups":
+            self._init_head_groups(plan)
+        else:
+            self._init_q_blocks(plan)
+        _LIVE.add(self)
+
+    def _init_head_groups(self, plan: AttentionPlan) -> None:
+        device = self.device
+        group = plan.q_heads // plan.kv_heads
+        g = plan.head_group_kv_heads
+        self.q, self.k, self.v, self.output = None, [], [], []
+        self.running_max = self.running_sum = self.accumulator = None
+        self.head_group_sets = [
+            (
+                torch.empty((plan.max_q_tokens, g * group, plan.head_dim), dtype=plan.dtype, device=device),
+                torch.empty((plan.max_kv_tokens, g, plan.head_dim), dtype=plan.dtype, device=device),
+                torch.empty((plan.max_kv_tokens, g, plan.head_dim), dtype=plan.dtype, device=device),
+                torch.empty(plan.head_group_vt_bytes, dtype=torch.uint8, device=device)
+                if plan.head_group_vt_bytes
+                else None,
+            )
+            for _ in range(plan.head_group_sets)
+        ]
+        sets = self.head_group_sets
+
+        def pointers(index):
+            return (ctypes.c_void_p * 2)(*[s[index].data_ptr() for s in sets])
+
+        vt = pointers(3) if plan.head_group_vt_bytes else None
+        handle = ctypes.c_void_p()
+        status = self._lib.sa_pipeline_create_head_groups(
+            ctypes.byref(handle),
+            device.index if device.index is not None else torch.cuda.current_device(),
+            pointers(0), pointers(1), pointers(2), vt, plan.head_group_vt_bytes, len(sets),
+            plan.max_q_tokens, plan.max_kv_tokens, g, plan.kv_chunk_tokens,
+            plan.q_heads, plan.kv_heads, plan.head_dim, _native.dtype_code(plan.dtype),
+            self.h2d_stream.cuda_stream, self.d2h_stream.cuda_stream,
+        )
+        _native.check(status, "sa_pipeline_create_head_groups")
+        self.handle = handle
+
+    def _init_q_blocks(self, plan: AttentionPlan) -> None:
+        device = self.device
+        self.head_group_sets = []
         self.q = torch.empty((plan.q_chunk_tokens, plan.q_heads, plan.head_dim), dtype=plan.dtype, device=device)
         self.k = [
             torch.empty((plan.kv_chunk_tokens, plan.kv_heads, plan.head_dim), dtype=plan.dtype, device=device)
@@ -88,13 +145,7 @@ class CudaWorkspace:
             if plan.output_mode == "host"
             else []
         )
-        self.compute_stream = torch.cuda.current_stream(device)
-        # Copy streams are torch streams (default priority) so torch's caching
-        # allocator can track their uses of workspace and consumer buffers
-        # (record_stream) for as long as those buffers live.
-        self.h2d_stream, self.d2h_stream = copy_streams(device)
-
-        lib = _native.lib()
+        lib = self._lib
         k_ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in self.k])
         v_ptrs = (ctypes.c_void_p * 3)(*[t.data_ptr() for t in self.v])
         out_ptrs = (ctypes.c_void_p * 2)(*[t.data_ptr() for t in self.output]) if self.output else None
@@ -110,11 +161,7 @@ class CudaWorkspace:
             self.h2d_stream.cuda_stream, self.d2h_stream.cuda_stream,
         )
         _native.check(status, "sa_pipeline_create")
-        self._lib = lib
         self.handle = handle
-        self.plan = plan
-        self.resident_scratch: torch.Tensor | None = None
-        _LIVE.add(self)
 
     def enable_trace_ranges(self) -> None:
         """Bracket each pipeline stage's enqueue with ROCm tracer ranges named

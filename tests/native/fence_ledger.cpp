@@ -157,6 +157,18 @@ hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKin
   return hipSuccess;
 }
 
+// A strided copy is recorded by the bounding range of its rows on each side:
+// the gaps between rows count as accessed, which can only add conflicts.
+hipError_t hipMemcpy2DAsync(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height,
+                            hipMemcpyKind kind, hipStream_t stream) {
+  const Kind k = kind == hipMemcpyHostToDevice ? kCopyH2D : kind == hipMemcpyDeviceToHost ? kCopyD2H : kCopyD2D;
+  const int64_t src_bytes = height ? (int64_t)((height - 1) * spitch + width) : 0;
+  const int64_t dst_bytes = height ? (int64_t)((height - 1) * dpitch + width) : 0;
+  push(Op{k, stream_id(stream), -1, {span(src, src_bytes)}, {span(dst, dst_bytes)},
+          k == kCopyH2D ? "h2d 2-d copy" : k == kCopyD2H ? "d2h 2-d copy" : "d2d 2-d copy"});
+  return hipSuccess;
+}
+
 // ------------------------------------------------------- kernel launchers
 namespace sa {
 

@@ -285,3 +285,115 @@ def test_a_dropped_wait_is_reported_in_host_aliased_runs(ledger):
         caught += ledger.ledger_check(None, 0) > 0
     print(f"host_aliased dropped-wait runs reported: {caught} of {waits}")
     assert caught >= waits * 3 // 4
+
+
+def run_head_groups(lib, *, num_sets, causal, q_lengths, k_lengths, group_kv, q_heads=4, kv_heads=2, head_dim=64,
+                    kv_chunk=256, with_vt=False, with_lse=True):
+    """One sa_pipeline_run on a head-group pipeline (every token of a group
+    of K/V heads per unit, buffer sets used in turn)."""
+    dev = Space(0x7000_0000_0000)
+    host = Space(0x5000_0000_0000)
+    group = q_heads // kv_heads
+    cu_q, q_b = bounds(q_lengths)
+    cu_k, k_b = bounds(k_lengths)
+    tq, tk = q_b[-1], k_b[-1]
+    qo = [dev.take(tq * group_kv * group * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+    ks = [dev.take(tk * group_kv * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+    vs = [dev.take(tk * group_kv * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+    vt_bytes = group_kv * 128 * (-(-max(k_lengths) // 64) * 64) * HEAD_BYTES if with_vt else 0
+    vts = (ctypes.c_void_p * 2)(*[dev.take(vt_bytes) for _ in range(num_sets)]) if with_vt else None
+    handle = ctypes.c_void_p()
+    status = lib.sa_pipeline_create_head_groups(
+        ctypes.byref(handle), 0, (ctypes.c_void_p * 2)(*qo), (ctypes.c_void_p * 2)(*ks), (ctypes.c_void_p * 2)(*vs),
+        vts, vt_bytes, num_sets, tq, tk, group_kv, kv_chunk, q_heads, kv_heads, head_dim, 0, None, None)
+    assert status == 0, lib.sa_last_error()
+    q_row, kv_row = q_heads * head_dim * HEAD_BYTES, kv_heads * head_dim * HEAD_BYTES
+    q_host, k_host, v_host = host.take(tq * q_row), host.take(tk * kv_row), host.take(tk * kv_row)
+    out_host = host.take(tq * q_row)
+    lse = dev.take(q_heads * tq * 4) if with_lse else None
+    stats = _native.PipelineStats()
+    status = lib.sa_pipeline_run(handle, q_host, k_host, v_host, out_host, lse, tq if with_lse else 0, cu_q, cu_k,
+                                 len(q_lengths), 0.125, int(causal), 0xC0FFEE, ctypes.byref(stats))
+    assert status == 0, lib.sa_last_error()
+    assert lib.sa_pipeline_destroy(handle) == 0
+    return stats
+
+
+HEAD_GROUP_CASES = [
+    # (q_heads, kv_heads, K/V heads per unit): MHA one head per unit, GQA
+    # with a short last group, all heads in one unit.
+    (4, 4, 1),
+    (8, 4, 3),
+    (6, 2, 2),
+]
+
+
+@pytest.mark.parametrize("num_sets", [1, 2])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("heads", HEAD_GROUP_CASES)
+def test_head_group_schedule_is_race_free(ledger, num_sets, causal, heads):
+    q_heads, kv_heads, group_kv = heads
+    for q_lengths, k_lengths in CASES:
+        ledger.ledger_reset()
+        stats = run_head_groups(ledger, num_sets=num_sets, causal=causal, q_lengths=q_lengths, k_lengths=k_lengths,
+                                group_kv=group_kv, q_heads=q_heads, kv_heads=kv_heads)
+        units = -(-kv_heads // group_kv)
+        row = q_heads * 64 * HEAD_BYTES
+        # Every byte of Q, K and V crosses the link once; the output once.
+        assert stats.h2d_bytes == sum(q_lengths) * row + 2 * sum(k_lengths) * kv_heads * 64 * HEAD_BYTES
+        assert stats.d2h_bytes == sum(q_lengths) * row
+        assert stats.q_chunks == units
+        counts = (ctypes.c_int64 * 4)()
+        ledger.ledger_counts(counts)
+        assert counts[0] == 3 * units and counts[1] == units
+        assert counts[2] == units * sum(1 for n in q_lengths if n > 0)
+        check(ledger, f"head groups sets={num_sets} causal={causal} heads={heads} q={q_lengths} k={k_lengths}")
+
+
+@pytest.mark.parametrize("num_sets", [1, 2])
+def test_head_group_schedule_with_transposed_v_is_race_free(ledger, num_sets):
+    ledger.ledger_reset()
+    run_head_groups(ledger, num_sets=num_sets, causal=True, q_lengths=[700, 0, 1900], k_lengths=[900, 40, 1300],
+                    group_kv=1, q_heads=8, kv_heads=4, head_dim=128, with_vt=True)
+    counts = (ctypes.c_int64 * 4)()
+    ledger.ledger_counts(counts)
+    assert counts[2] == 4 * 2 * 2  # per unit and non-empty segment: a transpose and an update launch
+    check(ledger, f"head groups with transposed V, sets={num_sets}")
+
+
+def test_a_dropped_wait_is_reported_in_head_group_runs(ledger):
+    # The waits that hold a set's next copies behind its previous output copy,
+    # a unit's launch behind its copies and the output copy behind the launch
+    # are all necessary; only the fork and join of the second stream can be
+    # implied by other orderings.
+    def run():
+        run_head_groups(ledger, num_sets=2, causal=False, q_lengths=[1500, 900], k_lengths=[1200, 900], group_kv=1,
+                        q_heads=4, kv_heads=4)
+
+    ledger.ledger_reset()
+    run()
+    check(ledger, "baseline")
+    waits = ledger.ledger_waits()
+    assert waits > 10
+    caught = 0
+    for n in range(waits):
+        ledger.ledger_reset()
+        ledger.ledger_drop_wait(n)
+        run()
+        assert ledger.ledger_dropped() == 1
+        caught += ledger.ledger_check(None, 0) > 0
+    print(f"head-group dropped-wait runs reported: {caught} of {waits}")
+    assert caught >= waits - 2
+
+
+def test_step_api_is_refused_on_head_group_pipelines(ledger):
+    dev = Space(0x7000_0000_0000)
+    bufs = (ctypes.c_void_p * 2)(dev.take(1 << 20), dev.take(1 << 20))
+    handle = ctypes.c_void_p()
+    assert ledger.sa_pipeline_create_head_groups(ctypes.byref(handle), 0, bufs, bufs, bufs, None, 0, 1, 1024, 1024, 1,
+                                                 256, 4, 4, 64, 0, None, None) == 0
+    assert ledger.sa_pipeline_load_q(handle, 0x5000_0000_0000, 16, 0xC0FFEE, None) == -4
+    assert b"head-group" in ledger.sa_last_error()
+    assert ledger.sa_pipeline_finalize(handle, 0, 16, None, 0, 0, 0xC0FFEE) == -4
+    assert ledger.sa_pipeline_release_q(handle, 0xC0FFEE) == -4
+    assert ledger.sa_pipeline_destroy(handle) == 0

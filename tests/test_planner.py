@@ -170,3 +170,84 @@ def test_measured_rates_pick_fewest_passes_on_a_slow_link_and_large_chunks_when_
     # Without rates the reference's choice stands (README.md:62).
     plain = build_plan(**shape, config=config)
     assert (plain.q_chunk_tokens, plain.kv_chunk_tokens, plain.estimated_seconds) == (28_416, 8_192, None)
+
+
+# Head-group schedule (config.schedule == "head_groups"): buffer sets holding
+# every token of a group of K/V heads.  Expected values are worked out from
+# the set layout: per K/V head, Q and the output over it (tokens x group x D
+# x 2 bytes), K and V (tokens x D x 2 each) and, for head_dim 128, V
+# transposed ([128][tokens rounded up to 64] x 2 bytes).
+
+
+def _hg(budget_gib, *, n=524_288, heads=56, kv_heads=None, head_dim=128, **cfg):
+    config = StreamingAttentionConfig(workspace_budget_bytes=int(budget_gib * 2**30), schedule="head_groups", **cfg)
+    return build_plan(q_heads=heads, kv_heads=kv_heads or heads, head_dim=head_dim, dtype=torch.bfloat16,
+                      device="cpu", max_q_tokens=n, max_kv_tokens=n, config=config)
+
+
+def test_head_group_plan_at_the_benchmark_shape():
+    plan = _hg(2)
+    per_head = 524_288 * 128 * 2  # one tensor's bytes for one head
+    assert plan.schedule == "head_groups"
+    # Two sets of one head with V transposed: 2 x 4 x 134 MB = 1.07 GB; two
+    # heads per set would need 2.15 GB.
+    assert (plan.head_group_sets, plan.head_group_kv_heads, plan.head_group_units) == (2, 1, 56)
+    assert plan.head_group_vt_bytes == per_head
+    assert plan.estimated_workspace_bytes == 2 * 4 * per_head + 32 * 2**20 <= 2 * 2**30
+    # The default schedule's K/V chunk (row sums merge there): same bits.
+    assert plan.kv_chunk_tokens == 8192
+    assert plan.q_chunk_tokens == 524_288 and plan.q_passes == 1
+
+
+def test_head_group_plan_drops_the_transposed_copy_before_the_second_set():
+    # 1 GiB: two sets with V transposed (1.07 GB + margin) do not fit, two
+    # without it (0.81 GB) do; the K/V chunk follows the default plan (4,096).
+    plan = _hg(1)
+    assert (plan.head_group_sets, plan.head_group_kv_heads, plan.head_group_vt_bytes) == (2, 1, 0)
+    assert plan.kv_chunk_tokens == 4096
+    # 0.5 GiB: one set of Q, K and V (403 MB) is all that fits.
+    plan = _hg(0.5)
+    assert (plan.head_group_sets, plan.head_group_kv_heads, plan.head_group_vt_bytes) == (1, 1, 0)
+
+
+def test_head_group_units_are_evened_out():
+    # 14 GiB fits 12 heads per set pair (12 x 1.07 GB = 12.9 GB); 56 heads in
+    # ceil(56 / 12) = 5 units, evened out to ceil(56 / 5) = 12 per unit.
+    plan = _hg(14)
+    assert (plan.head_group_kv_heads, plan.head_group_units) == (12, 5)
+    # GQA: a unit takes its K/V heads' query heads too (8 query heads per
+    # K/V head here), and the transposed copy is per K/V head.
+    plan = _hg(2, heads=64, kv_heads=8)
+    per_kv_head = 524_288 * 128 * 2 * (8 + 2 + 1)
+    fit = (2 * 2**30 - 32 * 2**20) // (2 * per_kv_head)
+    assert fit == 0
+    # one K/V head with its 8 query heads is 1.48 GB per set: one set only.
+    assert (plan.head_group_sets, plan.head_group_kv_heads) == (1, 1)
+
+
+def test_head_group_plan_without_budget_holds_every_head_and_rejects_tiny_budgets():
+    plan = build_plan(q_heads=8, kv_heads=2, head_dim=64, dtype=torch.bfloat16, device="cpu", max_q_tokens=4096,
+                      max_kv_tokens=4096, config=StreamingAttentionConfig(schedule="head_groups"))
+    assert (plan.head_group_sets, plan.head_group_kv_heads, plan.head_group_units, plan.head_group_vt_bytes) == (
+        2, 2, 1, 0)
+    with pytest.raises(ValueError, match="too small for the head-group schedule"):
+        _hg(0.25)
+
+
+def test_head_group_chunk_is_rounded_to_whole_tiles_when_segments_can_be_longer():
+    config = StreamingAttentionConfig(schedule="head_groups", kv_chunk_tokens=1000, block_n=16)
+    plan = build_plan(q_heads=4, kv_heads=4, head_dim=64, dtype=torch.bfloat16, device="cpu", max_q_tokens=5000,
+                      max_kv_tokens=5000, config=config)
+    assert plan.kv_chunk_tokens == 960
+    # A chunk covering every key needs no merge boundary and is kept.
+    plan = build_plan(q_heads=4, kv_heads=4, head_dim=64, dtype=torch.bfloat16, device="cpu", max_q_tokens=912,
+                      max_kv_tokens=912, config=config)
+    assert plan.kv_chunk_tokens == 912
+
+
+def test_schedule_validation():
+    with pytest.raises(ValueError, match="schedule must be"):
+        StreamingAttentionConfig(schedule="tiles").validate()
+    with pytest.raises(ValueError, match="device_consumer"):
+        StreamingAttentionConfig(schedule="head_groups", output_mode="device_consumer").validate()
+    StreamingAttentionConfig(schedule="head_groups", output_mode="host_aliased").validate()
