@@ -3,29 +3,37 @@
 Workload (one "step"): non-causal BF16 MHA over 524,288 tokens, 56 heads,
 head_dim 128, Q/K/V ~ N(0,1) (seeded per 4,096-token chunk like the reference
 benchmark) in caller-owned pinned DRAM, output back to caller-owned pinned
-DRAM, through a 2 GiB HBM workspace in the decomposition the planner picks:
-resident Q blocks of 28,416 tokens, 8,192-token K/V chunks, 19 passes over
-K/V, the final D2H included (the reference's
-src/seqattn_core/benchmarking/streaming.py:185-213 setting).  The LSE of every row is written too.  Each K/V chunk is applied by
-two concurrent launches, one per half of the Q block's rows, on two streams.
+DRAM through a 2 GiB HBM workspace, the final D2H included (the reference's
+src/seqattn_core/benchmarking/streaming.py:185-213 setting).  The LSE of
+every row is written too.
 
-``value`` is that pinned-DRAM step.  Beside it, from the same run:
+``value`` is that pinned-DRAM step in the head-group schedule (--schedule):
+the planner fits two buffer sets of one K/V head's every token (Q, K, V and
+V transposed) into the budget, so each byte of Q, K and V crosses PCIe once
+(22.5 GB per step instead of 293 GB for the reference's Q-block plan); each
+unit is one fused update launch over all query and key pairs of its head,
+consecutive units alternating between two streams while the next unit's
+strided copies land.  Beside it, from the same run:
 * roofline of the update kernel in that leg: algorithmic FLOP per step over
   the update kernels' busy time per step, the union of the launch intervals
-  timed with HIP events on the streams the launches run on (the two
-  concurrent halves of a chunk count once); traffic per chunk span is read
-  from the committed rocprofv3 counter summary of the same leg;
+  timed with HIP events on the streams the launches run on (overlapping
+  launches count once); traffic per launch is read from the committed
+  rocprofv3 counter summary of the same leg;
 * PCIe: logical H2D bytes per step over the step time, against a measured
   pinned H2D copy rate;
+* q_blocks: the same step in the reference planner's Q-block schedule (Q
+  blocks of 28,416 tokens, 8,192-token K/V chunks, 19 passes over K/V, each
+  chunk applied by two concurrent half-block launches);
 * resident_hbm: the same inputs already resident in HBM, one update launch per
   step over all queries and keys with the finalize fused (no PCIe);
+* host_aliased: the Q-block step with each pass's output finalized into its
+  Q block (no output slot in the budget, 14 passes instead of 19);
 * cpu_baseline: the CPU oracle (numpy restatement of the reference's chunked
   FP32 attention) timed on this host on a bounded row sample, which is also
-  the parity check of the sampled rows (O and LSE) of both legs;
-* host_aliased: the same pinned step with each pass's output finalized
-  into its Q block (no output slot in the budget, 14 passes instead of 19);
+  the parity check of the sampled rows (O and LSE) of every leg, and the
+  legs' bit-identity on those rows;
 * config2_65k, config4_paged and config5_1m: the benchmark's other
-  configurations, measured after the headline leg's buffers are released
+  configurations, measured after the headline legs' buffers are released
   (65,536 tokens x 32 heads resident and streamed with 1 GiB; 158,208
   tokens x 48 heads from a 256-token page store; 1,048,576 tokens x 64
   heads with peaked keys and an 8 GiB workspace, one step), each with
@@ -100,8 +108,16 @@ def parse_args():
                          "--steps; 0 skips it)")
     ap.add_argument("--resident-warmup", type=int, default=1,
                     help="warmup steps of the HBM-resident leg (at most --warmup)")
-    ap.add_argument("--traffic-file", type=Path,
-                    default=ROOT / "profiles" / "update_kernel_pinned_524k_56h_2gib_traffic.txt")
+    ap.add_argument("--traffic-file", type=Path, default=None,
+                    help="committed rocprofv3 counter summary of the headline leg's update kernel (default: "
+                         "the summary for --schedule under profiles/)")
+    ap.add_argument("--schedule", default="head_groups", choices=["head_groups", "q_blocks"],
+                    help="schedule of the headline pinned-DRAM leg (value): head_groups (every token of a "
+                         "group of K/V heads resident per unit; Q, K and V copied once) or q_blocks (the "
+                         "reference planner's Q super-blocks, K/V streamed once per block); the other "
+                         "schedule runs beside it as a side leg")
+    ap.add_argument("--other-schedule-steps", type=int, default=3,
+                    help="timed steps of the other schedule's pinned leg (at most --steps; 0 skips it)")
     ap.add_argument("--workload", default="streamed", choices=["streamed", "paged", "sweep", "1m", "65k", "projected"],
                     help="streamed: the headline 524,288-token run (default); paged: the 158,208-token "
                          "48-head paged run from an aligned on-disk page store; sweep: the 524,288-token "
@@ -391,20 +407,23 @@ def main() -> int:
     cu = torch.tensor([0, n], dtype=torch.int32)
     log(f"inputs ready in {time.perf_counter() - t0:.1f}s")
 
-    config = StreamingAttentionConfig(
-        workspace_budget_bytes=int(args.workspace_gib * 2**30),
-        kv_chunk_tokens=args.kv_chunk,
-        output_mode=args.output_mode,
-        backend="hip",
-        **({} if args.num_kv_buffers is None else {"num_kv_buffers": args.num_kv_buffers}),
-    )
-    plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
-                      max_q_tokens=n, max_kv_tokens=n, config=config)
-    runner = StreamingAttentionRunner(plan, config)
-    log(f"plan q_chunk={plan.q_chunk_tokens} kv_chunk={plan.kv_chunk_tokens} passes={plan.q_passes} "
-        f"workspace={plan.estimated_workspace_bytes / 2**30:.3f} GiB")
+    budget = int(args.workspace_gib * 2**30)
+    kv_buffers = {} if args.num_kv_buffers is None else {"num_kv_buffers": args.num_kv_buffers}
     lib = _native.lib()
-    handle = runner._workspace.handle
+
+    def make_runner(schedule, output_mode):
+        cfg = StreamingAttentionConfig(workspace_budget_bytes=budget, kv_chunk_tokens=args.kv_chunk,
+                                       output_mode=output_mode, backend="hip", schedule=schedule, **kv_buffers)
+        p = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
+                       max_q_tokens=n, max_kv_tokens=n, config=cfg)
+        if schedule == "head_groups":
+            log(f"plan {schedule}: {p.head_group_units} units of {p.head_group_kv_heads} K/V heads, "
+                f"{p.head_group_sets} buffer sets, transposed V {p.head_group_vt_bytes > 0}, "
+                f"kv_chunk={p.kv_chunk_tokens} workspace={p.estimated_workspace_bytes / 2**30:.3f} GiB")
+        else:
+            log(f"plan {schedule} ({output_mode}): q_chunk={p.q_chunk_tokens} kv_chunk={p.kv_chunk_tokens} "
+                f"passes={p.q_passes} workspace={p.estimated_workspace_bytes / 2**30:.3f} GiB")
+        return p, StreamingAttentionRunner(p, cfg)
 
     # Sampled rows of the parity check: the reference's signature rows plus
     # seeded-random rows.  Each leg's O and LSE on them are kept as it ends.
@@ -420,49 +439,96 @@ def main() -> int:
             idx = rows_t if out.device.type == "cpu" else rows_t.cuda()
             legs_out.append((leg, out[idx].cpu(), lse[:, rows_t.cuda()].cpu()))
 
-    # Headline: caller-owned pinned DRAM -> 2 GiB workspace -> pinned DRAM.
     out_host = torch.empty((n, h, d), dtype=torch.bfloat16, pin_memory=True)
-    lse_pinned = torch.empty((h, n), dtype=torch.float32, device="cuda")
-    stats = StreamingAttentionStats()
-    sec, busy_ms, sum_ms, launches = timed_steps(
-        lib, handle,
-        lambda i: runner(q, k, v, cu, cu, out=out_host, lse_out=lse_pinned, stats=stats if i is not None else None),
-        args.steps, args.warmup, "pinned",
-    )
-    value = flop / sec / 1e12
-    h2d_per_step = stats.h2d_bytes / args.steps
-    # Rows per pass: the plan's pass count with the rows spread evenly in
-    # multiples of the kernel's workgroup tile (the pipeline's schedule); one
-    # chunk span applies one K/V chunk to one pass's rows with two concurrent
-    # half-block launches.
-    rows_per_pass = stats.max_resident_q_tokens
-    spans_per_step = stats.kv_tiles // args.steps
-    busy_per_step_ms = busy_ms / args.steps
-    kernel_tflops = flop / (busy_per_step_ms / 1e3) / 1e12 if busy_ms > 0 else None
-    traffic = read_traffic(args.traffic_file)
-    pcie = {
-        "h2d_gb_per_step": round(h2d_per_step / 1e9, 2),
-        "h2d_achieved_gbps": round(h2d_per_step / sec / 1e9, 2),
-        "h2d_measured_gbps": round(h2d_peak, 2),
-        "h2d_frac": round(h2d_per_step / sec / 1e9 / h2d_peak, 4),
-        "d2h_gb_per_step": round(stats.d2h_bytes / args.steps / 1e9, 2),
-    }
-    log(f"pinned DRAM e2e: {value:.1f} TFLOPS, {sec:.3f} s/step, kernel busy {busy_per_step_ms:.1f} ms/step "
-        f"({kernel_tflops:.1f} TFLOPS), H2D {pcie['h2d_achieved_gbps']:.1f} GB/s")
-    keep_rows("pinned", out_host, lse_pinned)
+
+    def pinned_leg(schedule, output_mode, steps, warmup, label):
+        """Caller-owned pinned DRAM -> the budget's workspace -> pinned DRAM,
+        final D2H included, LSE written."""
+        p, r = make_runner(schedule, output_mode)
+        lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
+        st = StreamingAttentionStats()
+        sec, busy_ms, sum_ms, launches = timed_steps(
+            lib, r._workspace.handle,
+            lambda i: r(q, k, v, cu, cu, out=out_host, lse_out=lse, stats=st if i is not None else None),
+            steps, warmup, label,
+        )
+        keep_rows(label, out_host, lse)
+        r.close()
+        del r, lse
+        release_memory()
+        h2d = st.h2d_bytes / steps
+        busy = busy_ms / steps
+        leg = {
+            "value": round(flop / sec / 1e12, 2),
+            "unit": "TFLOPS",
+            "ms_per_step": round(sec * 1e3, 2),
+            "steps": steps,
+            "warmup": warmup,
+            "mfma_peak_frac": round(flop / sec / 1e12 / PEAK_BF16_TFLOPS, 4),
+            "kernel_tflops": round(flop / (busy / 1e3) / 1e12, 2) if busy > 0 else None,
+            "kernel_frac": round(flop / (busy / 1e3) / 1e12 / PEAK_BF16_TFLOPS, 4) if busy > 0 else None,
+            "kernel_busy_ms_per_step": round(busy, 2),
+            "update_launches_per_step": launches // steps,
+            "avg_launch_ms": round(sum_ms / max(launches, 1), 4),
+            "estimated_workspace_bytes": p.estimated_workspace_bytes,
+            "kv_chunk_tokens": p.kv_chunk_tokens,
+            "h2d_gb_per_step": round(h2d / 1e9, 2),
+            "h2d_achieved_gbps": round(h2d / sec / 1e9, 2),
+            "h2d_frac": round(h2d / sec / 1e9 / h2d_peak, 4),
+            "d2h_gb_per_step": round(st.d2h_bytes / steps / 1e9, 2),
+        }
+        if schedule == "head_groups":
+            leg.update({
+                "schedule": "head_groups",
+                "units": p.head_group_units,
+                "kv_heads_per_unit": p.head_group_kv_heads,
+                "buffer_sets": p.head_group_sets,
+                "transposed_v": p.head_group_vt_bytes > 0,
+                "workload": f"same inputs and {args.workspace_gib:g} GiB budget, head-group schedule: every "
+                            f"token of {p.head_group_kv_heads} K/V head(s) resident per unit, "
+                            f"{p.head_group_sets} buffer sets, Q/K/V copied once (strided copies), one fused "
+                            "update launch per unit writing output and LSE, units alternating between two "
+                            "streams",
+            })
+        else:
+            leg.update({
+                "schedule": "q_blocks",
+                "output_mode": output_mode,
+                "q_chunk_tokens": p.q_chunk_tokens,
+                "q_passes": p.q_passes,
+                "rows_per_pass": st.max_resident_q_tokens,
+                "spans_per_step": st.kv_tiles // steps,
+                "workload": f"same inputs and {args.workspace_gib:g} GiB budget, the reference planner's "
+                            f"Q-block schedule with output_mode='{output_mode}' (Q block {p.q_chunk_tokens:,}, "
+                            f"K/V chunk {p.kv_chunk_tokens:,}, {p.q_passes} passes over K/V; each chunk "
+                            "applied by two concurrent half-block launches)",
+            })
+        log(f"{label}: {leg['value']:.1f} TFLOPS, {sec:.3f} s/step, kernel busy {busy:.1f} ms/step "
+            f"({leg['kernel_tflops']} TFLOPS), H2D {leg['h2d_achieved_gbps']:.1f} GB/s")
+        return p, leg
+
+    # Headline: the schedule named by --schedule; the other one beside it.
+    other = "q_blocks" if args.schedule == "head_groups" else "head_groups"
+    plan, head = pinned_leg(args.schedule, args.output_mode, args.steps, args.warmup, args.schedule)
+    value = head["value"]
+    sec = head["ms_per_step"] / 1e3
+    side_legs = {}
+    o_steps = min(args.other_schedule_steps, args.steps)
+    if o_steps > 0:
+        side_legs[other] = pinned_leg(other, "host", o_steps, min(1, args.warmup), other)[1]
 
     resident = None
-    out_dev = lse_res = None
     if "resident" in legs:
         # The same inputs already in HBM: one update launch per step over all
         # queries and keys, finalize fused, no PCIe.
+        r_plan, r_runner = make_runner("q_blocks", "host")
         qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
         out_dev = torch.empty_like(qd)
-        lse_res = torch.empty_like(lse_pinned)
+        lse_res = torch.empty((h, n), dtype=torch.float32, device="cuda")
         r_steps = max(1, min(args.resident_steps, args.steps))
         r_warm = min(args.resident_warmup, args.warmup)
         r_sec, r_busy, r_sum, r_launches = timed_steps(
-            lib, handle, lambda i: runner(qd, kd, vd, cu, cu, out=out_dev, lse_out=lse_res),
+            lib, r_runner._workspace.handle, lambda i: r_runner(qd, kd, vd, cu, cu, out=out_dev, lse_out=lse_res),
             r_steps, r_warm, "resident",
         )
         resident = {
@@ -478,57 +544,19 @@ def main() -> int:
                         "one update launch per step with the finalize fused",
         }
         keep_rows("resident", out_dev, lse_res)
-        del qd, kd, vd, out_dev
+        r_runner.close()
+        del qd, kd, vd, out_dev, lse_res, r_runner
         release_memory()
         log(f"resident: {resident['value']:.1f} TFLOPS, {r_sec:.3f} s/step")
 
     aliased = None
-    if args.aliased_steps > 0:
-        # The same pinned-DRAM step with output_mode="host_aliased": each
-        # pass's output is finalized into its own Q block, so the budget
-        # holds no output slot, the Q block is larger and there are fewer
-        # passes over K/V (less H2D).  Same inputs, same output buffer.
-        a_config = StreamingAttentionConfig(workspace_budget_bytes=int(args.workspace_gib * 2**30),
-                                            kv_chunk_tokens=args.kv_chunk, output_mode="host_aliased",
-                                            backend="hip")
-        a_plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
-                            max_q_tokens=n, max_kv_tokens=n, config=a_config)
-        a_runner = StreamingAttentionRunner(a_plan, a_config)
-        a_stats = StreamingAttentionStats()
-        a_lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
-        a_steps = min(args.aliased_steps, args.steps)
-        a_warm = min(1, args.warmup)
-        a_sec, a_busy, _, a_launches = timed_steps(
-            lib, a_runner._workspace.handle,
-            lambda i: a_runner(q, k, v, cu, cu, out=out_host, lse_out=a_lse, stats=a_stats if i is not None else None),
-            a_steps, a_warm, "aliased",
-        )
-        a_h2d = a_stats.h2d_bytes / a_steps
-        aliased = {
-            "value": round(flop / a_sec / 1e12, 2),
-            "unit": "TFLOPS",
-            "ms_per_step": round(a_sec * 1e3, 2),
-            "steps": a_steps,
-            "warmup": a_warm,
-            "mfma_peak_frac": round(flop / a_sec / 1e12 / PEAK_BF16_TFLOPS, 4),
-            "kernel_tflops": round(flop / (a_busy / a_steps / 1e3) / 1e12, 2) if a_busy > 0 else None,
-            "q_chunk_tokens": a_plan.q_chunk_tokens,
-            "kv_chunk_tokens": a_plan.kv_chunk_tokens,
-            "q_passes": a_plan.q_passes,
-            "estimated_workspace_bytes": a_plan.estimated_workspace_bytes,
-            "update_launches_per_step": a_launches // a_steps,
-            "h2d_gb_per_step": round(a_h2d / 1e9, 2),
-            "h2d_achieved_gbps": round(a_h2d / a_sec / 1e9, 2),
-            "h2d_frac": round(a_h2d / a_sec / 1e9 / h2d_peak, 4),
-            "workload": "same pinned-DRAM step and 2 GiB budget with output_mode='host_aliased' (output "
-                        "finalized into the pass's Q block, no output slot)",
-        }
-        keep_rows("aliased", out_host, a_lse)
-        a_runner.close()
-        del a_runner, a_lse
-        release_memory()
-        log(f"aliased: {aliased['value']:.1f} TFLOPS, {a_sec:.3f} s/step, {a_plan.q_passes} passes, "
-            f"H2D {aliased['h2d_achieved_gbps']:.1f} GB/s")
+    a_steps = min(args.aliased_steps, args.steps)
+    if a_steps > 0:
+        # The Q-block schedule with output_mode="host_aliased": each pass's
+        # output is finalized into its own Q block, so the budget holds no
+        # output slot, the Q block is larger and there are fewer passes over
+        # K/V (less H2D).  Same inputs, same output buffer.
+        aliased = pinned_leg("q_blocks", "host_aliased", a_steps, min(1, args.warmup), "aliased")[1]
 
     parity = None
     cpu_baseline = None
@@ -604,7 +632,58 @@ def main() -> int:
         log(f"parity max|dO| = {err_o:.3e} max|dLSE| = {err_l:.3e} {errors} relL2 {rel_l2}; "
             f"CPU oracle {cpu_tflops:.4f} TFLOPS on {threads} threads")
 
-    flop_per_span = flop / max(spans_per_step, 1)  # the average over the passes' row counts
+    kernel_tflops = head["kernel_tflops"]
+    traffic_file = args.traffic_file
+    if traffic_file is None:
+        traffic_file = ROOT / "profiles" / (
+            "update_kernel_head_groups_524k_56h_2gib_traffic.txt" if args.schedule == "head_groups"
+            else "update_kernel_pinned_524k_56h_2gib_traffic.txt")
+    if args.schedule == "head_groups":
+        # One unit of kernel work: a unit's fused launch over all query and
+        # key pairs of its heads.
+        units = head["update_launches_per_step"]
+        roofline = {
+            "kernel": "update kernel in the head-group leg: one fused launch per unit (every query and key of "
+                      f"{plan.head_group_kv_heads} head(s)), consecutive units' launches on two streams, bf16 MFMA",
+            "traffic_unit": "HBM bytes per unit launch",
+            "flop_per_launch": round(flop / max(units, 1)),
+            "launches_per_step": units,
+        }
+        workload = (f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}, caller-owned pinned DRAM to "
+                    f"pinned DRAM (final D2H included, LSE written), {args.workspace_gib:g} GiB planner workspace, "
+                    f"head-group schedule ({plan.head_group_units} units of {plan.head_group_kv_heads} K/V head, "
+                    f"{plan.head_group_sets} buffer sets; Q, K and V each copied once)")
+        config_keys = {"schedule": "head_groups", "units": plan.head_group_units,
+                       "kv_heads_per_unit": plan.head_group_kv_heads, "buffer_sets": plan.head_group_sets,
+                       "transposed_v": plan.head_group_vt_bytes > 0, "kv_chunk_tokens": plan.kv_chunk_tokens}
+    else:
+        spans = head["spans_per_step"]
+        roofline = {
+            "kernel": "update_kernel in the pinned leg: each K/V chunk applied to a pass's Q rows by two "
+                      "concurrent half-block launches (one chunk span), bf16 MFMA",
+            "traffic_unit": "HBM bytes per chunk span (both half launches)",
+            "flop_per_span": round(flop / max(spans, 1)),
+            "spans_per_step": spans,
+            "avg_span_ms": round(head["kernel_busy_ms_per_step"] / max(spans, 1), 4),
+        }
+        workload = (f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}, caller-owned pinned DRAM to "
+                    f"pinned DRAM (final D2H included, LSE written), {args.workspace_gib:g} GiB planner workspace "
+                    f"(Q block {plan.q_chunk_tokens:,}, K/V chunk {plan.kv_chunk_tokens:,}, {plan.q_passes} passes)")
+        config_keys = {"schedule": "q_blocks", "output_mode": args.output_mode, "q_chunk_tokens": plan.q_chunk_tokens,
+                       "kv_chunk_tokens": plan.kv_chunk_tokens, "num_kv_buffers": plan.num_kv_buffers,
+                       "q_passes": plan.q_passes, "rows_per_pass": head["rows_per_pass"]}
+    roofline.update({
+        "bound": "mfma",
+        "achieved": kernel_tflops,
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": head["kernel_frac"],
+        "traffic": read_traffic(traffic_file),
+        "kernel_busy_ms_per_step": head["kernel_busy_ms_per_step"],
+        "update_launches_per_step": head["update_launches_per_step"],
+        "avg_launch_ms": head["avg_launch_ms"],
+        "busy_definition": "union of the update launches' intervals (HIP events on each launch's stream)",
+    })
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -619,53 +698,33 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic: Q/K/V ~ N(0,1) bf16, seeded per 4,096-token chunk",
         "config": {
-            "workload": f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}, caller-owned pinned DRAM to "
-                        f"pinned DRAM (final D2H included, LSE written), {args.workspace_gib:g} GiB planner "
-                        f"workspace (Q block {plan.q_chunk_tokens:,}, K/V chunk {plan.kv_chunk_tokens:,}, "
-                        f"{plan.q_passes} passes)",
+            "workload": workload,
             "tokens": n,
             "heads": h,
             "head_dim": d,
             "workspace_gib": args.workspace_gib,
-            "output_mode": args.output_mode,
-            "q_chunk_tokens": plan.q_chunk_tokens,
-            "kv_chunk_tokens": plan.kv_chunk_tokens,
-            "num_kv_buffers": plan.num_kv_buffers,
-            "q_passes": plan.q_passes,
-            "rows_per_pass": rows_per_pass,
+            **config_keys,
             "estimated_workspace_bytes": plan.estimated_workspace_bytes,
         },
         "mfma_peak_frac": round(value / PEAK_BF16_TFLOPS, 4),
         "vs_published_rtx5090": round(value / PUBLISHED_TFLOPS, 3),
-        "roofline": {
-            "kernel": "update_kernel in the pinned leg: each K/V chunk applied to a pass's Q rows by two "
-                      "concurrent half-block launches (one chunk span), bf16 MFMA",
-            "bound": "mfma",
-            "achieved": round(kernel_tflops, 2) if kernel_tflops else None,
-            "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s",
-            "frac": round(kernel_tflops / PEAK_BF16_TFLOPS, 4) if kernel_tflops else None,
-            "traffic": traffic,
-            "traffic_unit": "HBM bytes per chunk span (both half launches)",
-            "flop_per_span": round(flop_per_span),
-            "spans_per_step": spans_per_step,
-            "avg_span_ms": round(busy_per_step_ms / max(spans_per_step, 1), 4),
-            "kernel_busy_ms_per_step": round(busy_per_step_ms, 2),
-            "update_launches_per_step": launches // args.steps,
-            "avg_launch_ms": round(sum_ms / max(launches, 1), 4),
-            "busy_definition": "union of the update launches' intervals (HIP events on each launch's stream)",
+        "roofline": roofline,
+        "pcie": {
+            "h2d_gb_per_step": head["h2d_gb_per_step"],
+            "h2d_achieved_gbps": head["h2d_achieved_gbps"],
+            "h2d_measured_gbps": round(h2d_peak, 2),
+            "h2d_frac": head["h2d_frac"],
+            "d2h_gb_per_step": head["d2h_gb_per_step"],
         },
-        "pcie": pcie,
+        other: side_legs.get(other),
         "resident_hbm": resident,
         "host_aliased": aliased,
         "cpu_baseline": cpu_baseline,
         "parity": parity,
     }
-    # Release the pipeline, the device buffers and the page-locked host
-    # buffers before the side workloads (and before the interpreter shuts
-    # down).
-    runner.close()
-    del out_host, lse_pinned, lse_res, q, k, v, runner, legs_out
+    # Release the device buffers and the page-locked host buffers before the
+    # side workloads (and before the interpreter shuts down).
+    del out_host, q, k, v, legs_out
     release_memory()
     if args.ceiling_seconds > 0:
         log("sustained-rate references: register-only MFMA probe and vendor bf16 GEMM")
