@@ -752,7 +752,7 @@ def measure_1m_in_child(args, steps, warmup, h2d_peak=None) -> dict:
 
     cmd = [sys.executable, "-u", str(Path(__file__).resolve()), "--workload", "1m", "--steps", str(steps),
            "--warmup", str(warmup), "--parity-rows", str(args.parity_rows), "--seed", str(args.seed),
-           "--cpu-workers", str(args.cpu_workers)]
+           "--cpu-workers", str(args.cpu_workers), "--schedule", args.schedule]
     if args.no_parity:
         cmd.append("--no-parity")
     done = subprocess.run(cmd, stdout=subprocess.PIPE, text=True, timeout=900)
@@ -848,9 +848,11 @@ def compare_sample(out, lse, rows, ref_o, ref_l) -> dict:
     return parity
 
 
-def run_pinned(q, k, v, cu, budget_gib, kv_chunk, steps, warmup, lse=None, output_mode="host", out=None):
+def run_pinned(q, k, v, cu, budget_gib, kv_chunk, steps, warmup, lse=None, output_mode="host", out=None,
+               schedule="q_blocks"):
     """Pinned-DRAM -> pinned-DRAM runs with the planner's plan for the budget
-    (``out``: a caller-provided host output; page-locked unless stated)."""
+    and schedule (``out``: a caller-provided host output; page-locked unless
+    stated)."""
     import torch
 
     from seqattn import StreamingAttentionConfig, StreamingAttentionRunner, StreamingAttentionStats, build_plan
@@ -858,19 +860,22 @@ def run_pinned(q, k, v, cu, budget_gib, kv_chunk, steps, warmup, lse=None, outpu
     n, h, d = q.shape
     pinned_out = out is None or out.is_pinned()
     config = StreamingAttentionConfig(workspace_budget_bytes=int(budget_gib * 2**30), kv_chunk_tokens=kv_chunk,
-                                      backend="hip", output_mode=output_mode, pin_output=pinned_out)
+                                      backend="hip", output_mode=output_mode, pin_output=pinned_out,
+                                      schedule=schedule)
     plan = build_plan(q_heads=h, kv_heads=k.shape[1], head_dim=d, dtype=q.dtype, device="cuda",
                       max_q_tokens=n, max_kv_tokens=k.shape[0], config=config)
     runner = StreamingAttentionRunner(plan, config)
     if out is None:
         out = torch.empty((n, h, d), dtype=q.dtype, pin_memory=True)
-    for _ in range(warmup):
+    for i in range(warmup):
         runner(q, k, v, cu, cu, out=out, lse_out=lse)
+        log(f"{n} tokens, {budget_gib:g} GiB, {schedule}: warmup {i + 1}/{warmup} done")
     torch.cuda.synchronize()
     stats = StreamingAttentionStats()
     t0 = time.perf_counter()
-    for _ in range(steps):
+    for i in range(steps):
         runner(q, k, v, cu, cu, out=out, stats=stats, lse_out=lse)
+        log(f"{n} tokens, {budget_gib:g} GiB, {schedule}: step {i + 1}/{steps} done")
     torch.cuda.synchronize()
     sec = (time.perf_counter() - t0) / steps
     runner.close()
@@ -904,14 +909,16 @@ def sweep_main(args) -> int:
     host_out = torch.empty((n, h, d), dtype=q.dtype, pin_memory=True)
     lse = torch.empty((h, n), dtype=torch.float32, device="cuda")
     all_ok = True
-    for gib in (1, 2, 4, 8, 14):
+    for gib, schedule in ((g, s) for g in (1, 2, 4, 8, 14) for s in ("q_blocks", "head_groups")):
         gc.collect()
         torch.cuda.empty_cache()
-        plan, out, stats, sec = run_pinned(q, k, v, cu, gib, None, args.steps, args.warmup, lse=lse, out=host_out)
+        plan, out, stats, sec = run_pinned(q, k, v, cu, gib, None, args.steps, args.warmup, lse=lse, out=host_out,
+                                           schedule=schedule)
         tflops = flop / sec / 1e12
         h2d_gbps = stats.h2d_bytes / args.steps / sec / 1e9
-        rows.append({"workspace_gib": gib, "q_chunk_tokens": plan.q_chunk_tokens,
+        rows.append({"workspace_gib": gib, "schedule": schedule, "q_chunk_tokens": plan.q_chunk_tokens,
                      "kv_chunk_tokens": plan.kv_chunk_tokens, "q_passes": plan.q_passes,
+                     "head_group_units": plan.head_group_units,
                      "h2d_gib_per_step": round(stats.h2d_bytes / args.steps / 2**30, 1),
                      "seconds_per_step": round(sec, 3), "tflops": round(tflops, 1),
                      "mfma_peak_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
@@ -926,7 +933,7 @@ def sweep_main(args) -> int:
             all_ok = all_ok and rows[-1]["parity"]["ok"]
         log(f"sweep {gib} GiB: {rows[-1]}")
         del out
-    two = next(r for r in rows if r["workspace_gib"] == 2)
+    two = next(r for r in rows if r["workspace_gib"] == 2 and r["schedule"] == args.schedule)
     result = {
         "metric": "effective TFLOPS, 524K-tok BF16 MHA from pinned DRAM to pinned DRAM, workspace sweep",
         "value": two["tflops"], "unit": "TFLOPS", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -934,7 +941,8 @@ def sweep_main(args) -> int:
         "vs_baseline": round(two["tflops"] / PUBLISHED_TFLOPS, 3), "dtype": "bf16",
         "data": "synthetic: Q/K/V ~ N(0,1) bf16 in pinned DRAM, seeded per 4,096-token chunk",
         "config": {"workload": f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}, pinned DRAM to "
-                               "pinned DRAM incl. final D2H; value at the 2 GiB workspace"},
+                               "pinned DRAM incl. final D2H; each budget with the reference planner's Q-block "
+                               f"schedule and the head-group schedule; value at the 2 GiB workspace, {args.schedule}"},
         "h2d_measured_gbps": round(h2d_peak, 1),
         "sweep": rows,
         "parity_ok": all_ok if not args.no_parity else None,
@@ -973,11 +981,15 @@ def measure_1m(args, steps, warmup, h2d_peak=None) -> dict:
         # A fourth 16 GiB page-locked buffer can exceed the host's pinning limit.
         out = torch.empty((n, h, d), dtype=torch.bfloat16)
         out_kind = "pageable host memory (page-locking a fourth 16 GiB buffer failed)"
-    log(f"1m: output in {out_kind}")
-    plan, out, stats, sec = run_pinned(q, k, v, cu, 8, 8192, steps, warmup, lse=lse, out=out)
+    # The head-group schedule's strided output copies need a page-locked out.
+    schedule = args.schedule if out.is_pinned() else "q_blocks"
+    log(f"1m: output in {out_kind}, {schedule} schedule")
+    plan, out, stats, sec = run_pinned(q, k, v, cu, 8, 8192, steps, warmup, lse=lse, out=out,
+                                       schedule=schedule)
     tflops = flop / sec / 1e12
     h2d_gbps = stats.h2d_bytes / steps / sec / 1e9
-    log(f"1m: {tflops:.1f} TFLOPS, {sec:.2f} s/step, passes {plan.q_passes}")
+    log(f"1m: {tflops:.1f} TFLOPS, {sec:.2f} s/step, {schedule}, passes {plan.q_passes}, "
+        f"units {plan.head_group_units}")
     parity = cpu_baseline = None
     if not args.no_parity:
         rng = np.random.default_rng(args.seed)
@@ -995,10 +1007,12 @@ def measure_1m(args, steps, warmup, h2d_peak=None) -> dict:
         "dtype": "bf16",
         "data": "synthetic: Q, V ~ N(0,1); K ~ N(0,1) x per-head U[0.5, 4]; bf16, seeded per 4,096-token chunk",
         "config": {"workload": f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}, Q/K/V in pinned "
-                               "DRAM, 8 GiB workspace, K/V chunk 8,192, LSE written, final D2H included",
-                   "output": out_kind,
+                               "DRAM, 8 GiB workspace, K/V chunk 8,192, LSE written, final D2H included, "
+                               f"{schedule} schedule",
+                   "output": out_kind, "schedule": schedule,
                    "q_chunk_tokens": plan.q_chunk_tokens, "kv_chunk_tokens": plan.kv_chunk_tokens,
-                   "q_passes": plan.q_passes},
+                   "q_passes": plan.q_passes, "head_group_units": plan.head_group_units,
+                   "kv_heads_per_unit": plan.head_group_kv_heads},
         "mfma_peak_frac": round(tflops / PEAK_BF16_TFLOPS, 4),
         "pcie": {"h2d_gb_per_step": round(stats.h2d_bytes / steps / 1e9, 1),
                  "h2d_achieved_gbps": round(h2d_gbps, 1),
@@ -1032,8 +1046,9 @@ def measure_65k(args, steps, warmup, h2d_peak=None) -> dict:
     q, k, v = make_inputs(n, h, d, args.seed)
     cu = torch.tensor([0, n], dtype=torch.int32)
     lse_s = torch.empty((h, n), dtype=torch.float32, device="cuda")
-    plan, out_s, stats, sec_s = run_pinned(q, k, v, cu, 1, 4096, steps, warmup, lse=lse_s)
-    config = StreamingAttentionConfig(workspace_budget_bytes=2**30, kv_chunk_tokens=4096, backend="hip")
+    plan, out_s, stats, sec_s = run_pinned(q, k, v, cu, 1, 4096, steps, warmup, lse=lse_s, schedule=args.schedule)
+    config = StreamingAttentionConfig(workspace_budget_bytes=2**30, kv_chunk_tokens=4096, backend="hip",
+                                      schedule=args.schedule)
     runner = StreamingAttentionRunner(plan, config)
     qd, kd, vd = q.cuda(), k.cuda(), v.cuda()
     out_r = torch.empty_like(qd)
@@ -1066,8 +1081,10 @@ def measure_65k(args, steps, warmup, h2d_peak=None) -> dict:
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic: Q/K/V ~ N(0,1) bf16 seeded per 4,096-token chunk",
         "config": {"workload": f"{n:,}-token non-causal BF16 MHA, {h} heads, head_dim {d}; value: Q/K/V "
-                               "resident in HBM; streamed: pinned DRAM with a 1 GiB workspace, K/V chunk 4,096",
-                   "q_chunk_tokens": plan.q_chunk_tokens, "q_passes": plan.q_passes},
+                               "resident in HBM; streamed: pinned DRAM with a 1 GiB workspace, K/V chunk 4,096, "
+                               f"{args.schedule} schedule",
+                   "schedule": args.schedule, "q_chunk_tokens": plan.q_chunk_tokens, "q_passes": plan.q_passes,
+                   "head_group_units": plan.head_group_units},
         "mfma_peak_frac": round(flop / sec_r / 1e12 / PEAK_BF16_TFLOPS, 4),
         "streamed_1gib": {"tflops": round(flop / sec_s / 1e12, 2), "ms_per_step": round(sec_s * 1e3, 2),
                           "mfma_peak_frac": round(flop / sec_s / 1e12 / PEAK_BF16_TFLOPS, 4),

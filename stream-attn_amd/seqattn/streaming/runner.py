@@ -11,10 +11,10 @@ signatures and validation as the reference.  Additive options:
 * q, k and v may be device tensors on the plan's device (HBM-resident
   inputs): the same Q super-block / K/V chunk schedule then reads them in
   place, nothing crosses PCIe and the output is a device tensor.
-* A plan of the head-group schedule (``schedule="head_groups"``) runs host
-  inputs into a host ``out`` with one native call per run, each byte of Q,
-  K and V crossing PCIe once; device outputs and ``run_with_device_output``
-  need the default schedule.
+* A plan of the head-group schedule (``schedule="head_groups"``) runs
+  page-locked host inputs into a page-locked host ``out`` with one native
+  call per run, each byte of Q, K and V crossing PCIe once; device outputs
+  and ``run_with_device_output`` need the default schedule.
 """
 
 from __future__ import annotations
@@ -143,9 +143,15 @@ class StreamingAttentionRunner(HipExecutorMixin):
         if out.shape != q_cpu.shape or out.dtype != q_cpu.dtype or out.device.type not in {"cpu", "cuda"}:
             raise ValueError("out must be a CPU tensor matching q shape and dtype")
         self._prepare_io(q_cpu, k_cpu, v_cpu, out)
-        if out.device.type != "cpu" and self.plan.schedule == "head_groups":
-            raise ValueError("schedule='head_groups' returns the output to host memory; "
-                             "a device out needs schedule='q_blocks'")
+        if self.plan.schedule == "head_groups":
+            if out.device.type != "cpu":
+                raise ValueError("schedule='head_groups' returns the output to host memory; "
+                                 "a device out needs schedule='q_blocks'")
+            if not all(t.is_pinned() for t in (q_cpu, k_cpu, v_cpu, out)):
+                # Strided copies between pageable memory and the device are
+                # staged by the runtime row by row.
+                raise ValueError("schedule='head_groups' copies head columns with strided copies, which need "
+                                 "page-locked q, k, v and out")
         lse = self._lse_buffer(q_cpu.shape[0], lse_out, return_lse)
         stats = self._prepare_stats(stats)
         started = time.perf_counter()
