@@ -232,6 +232,21 @@ int32_t sa_pipeline_create_head_groups(
     int32_t kv_chunk_tokens, int32_t q_heads, int32_t kv_heads, int32_t head_dim, int32_t dtype,
     void* h2d_stream, void* d2h_stream);
 
+/*
+ * Head-group pipelines only: page-locked host memory through which
+ * sa_pipeline_run copies the output when out_host is pageable (strided
+ * copies between pageable memory and the device are staged by the runtime
+ * row by row).  Each unit's output goes through it in row chunks, in order
+ * on the D2H stream: a chunk's copy, then a host function
+ * (hipLaunchHostFunc) that scatters the chunk into the host rows, then the
+ * next chunk; the calling thread does not wait for them until the run ends.
+ * The buffer must hold at least one output row of a unit
+ * (group_kv_heads * q_heads / kv_heads * head_dim * 2 bytes).  NULL and 0
+ * detach it; the pipeline keeps the pointer until then.  No counterpart in
+ * the reference.
+ */
+int32_t sa_pipeline_attach_host_staging(sa_pipeline* pipeline, void* staging, int64_t bytes);
+
 /* Wait for all pending copies of the pipeline, then release its events and the streams it created. */
 int32_t sa_pipeline_destroy(sa_pipeline* pipeline);
 

@@ -176,6 +176,10 @@ struct sa_pipeline {
   void* set_qo[kMaxSets] = {}, *set_k[kMaxSets] = {}, *set_v[kMaxSets] = {}, *set_vt[kMaxSets] = {};
   hipEvent_t set_ready[kMaxSets] = {}, set_done[kMaxSets] = {}, set_free[kMaxSets] = {};
   bool set_pending[kMaxSets] = {false, false};
+  // Page-locked host staging for a pageable output
+  // (sa_pipeline_attach_host_staging).
+  void* staging = nullptr;
+  int64_t staging_bytes = 0;
 
   // Host-side trace ranges around each stage's enqueue (sa_pipeline_set_trace_ranges).
   bool trace = false;
@@ -989,6 +993,21 @@ int32_t launch_unit(sa_pipeline* p, const void* q, int64_t sq_t, const void* k, 
   return 0;
 }
 
+// One chunk of a staged output: `rows` rows of `width` bytes from the dense
+// staging buffer into host rows `pitch` bytes apart.
+struct ScatterRows {
+  char* dst;
+  int64_t pitch;
+  const char* src;
+  int64_t width, rows;
+};
+
+// Host function of the D2H stream (it calls no HIP function).
+void scatter_rows(void* arg) {
+  const ScatterRows* s = static_cast<const ScatterRows*>(arg);
+  for (int64_t r = 0; r < s->rows; ++r) std::memcpy(s->dst + r * s->pitch, s->src + r * s->width, (size_t)s->width);
+}
+
 // sa_pipeline_run on a head-group pipeline.  Unit u (K/V heads
 // [u * group_kv, ...), with their query heads) uses buffer set u % num_sets
 // and, with two sets, compute stream u % 2 (the caller's, then the
@@ -1005,6 +1024,13 @@ int32_t launch_unit(sa_pipeline* p, const void* q, int64_t sq_t, const void* k, 
 // drain, and its copies landed during unit u.  Each launch is the one
 // sa_pipeline_run_resident makes for those heads, which the per-chunk
 // schedule matches bit for bit.
+//
+// Units are enqueued num_sets - 1 ahead of the unit whose output is being
+// copied out: a unit's copies into a set wait for the set's previous output
+// copy, so that copy has to be enqueued first.  With host staging attached
+// (a pageable output), the output of a unit goes through the staging buffer
+// in row chunks on the D2H stream, each scattered into the host rows by a
+// host function once its copy has landed, while later units' launches run.
 int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const char* vh, char* oh, float* lse,
                         int64_t lse_sh, const int64_t* cu_q, const int64_t* cu_k, int32_t num_segments,
                         double scale, int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
@@ -1025,6 +1051,11 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
   const int64_t total_q = cu_q[num_segments], total_k = cu_k[num_segments];
   const int group = p->q_heads / p->kv_heads;
   const int64_t d_bytes = (int64_t)p->head_dim * 2;
+  if (p->staging != nullptr && (int64_t)p->group_kv * group * d_bytes > p->staging_bytes) {
+    sa::set_error("sa_pipeline_run: host staging of %lld bytes cannot hold one output row of a unit "
+                  "(%lld bytes)", (long long)p->staging_bytes, (long long)p->group_kv * group * d_bytes);
+    return SA_ERR_INVALID_ARGUMENT;
+  }
   const int64_t q_pitch = p->q_heads * d_bytes, kv_pitch = p->kv_heads * d_bytes;
   const int units = (p->kv_heads + p->group_kv - 1) / p->group_kv;
   hipStream_t streams[sa_pipeline::kMaxSets] = {compute, p->side};
@@ -1035,13 +1066,39 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
     SA_HIP_RETURN(hipStreamWaitEvent(p->side, p->fork, 0));
     join.active = true;
   }
-  for (int u = 0; u < units; ++u) {
+  // Arguments of the staged output's host functions: they run after this
+  // function has enqueued them, and it returns only after the D2H stream has
+  // drained, so they live here; reserved in full so none moves.
+  std::vector<ScatterRows> scatters;
+  if (p->staging != nullptr) {
+    int64_t count = 0;
+    for (int u = 0; u < units; ++u) {
+      const int64_t wq = (int64_t)std::min(p->group_kv, p->kv_heads - u * p->group_kv) * group * d_bytes;
+      count += (total_q + p->staging_bytes / wq - 1) / (p->staging_bytes / wq);
+    }
+    scatters.reserve((size_t)count);
+  }
+  // Drains the D2H stream on every return (an error included) before the
+  // host functions' arguments above go away.
+  struct DrainD2H {
+    hipStream_t stream;
+    ~DrainD2H() { (void)hipStreamSynchronize(stream); }
+  } drain{p->d2h};
+  // K/V heads [kv0, kv0 + gk) of unit u and the bytes of one row of its
+  // Q/output (wq) and of its K and V (wk).
+  auto unit_heads = [&](int u, int* kv0, int* gk, int64_t* wq, int64_t* wk) {
+    *kv0 = u * p->group_kv;
+    *gk = std::min(p->group_kv, p->kv_heads - *kv0);
+    *wq = *gk * group * d_bytes;
+    *wk = *gk * d_bytes;
+  };
+  auto enqueue_unit = [&](int u) -> int32_t {
     const int b = u % p->num_sets;
     hipStream_t cs = streams[b];
-    const int kv0 = u * p->group_kv;
-    const int gk = std::min(p->group_kv, p->kv_heads - kv0);
+    int kv0, gk;
+    int64_t wq, wk;
+    unit_heads(u, &kv0, &gk, &wq, &wk);
     const int gq = gk * group;
-    const int64_t wq = gq * d_bytes, wk = gk * d_bytes;
     char* qo = static_cast<char*>(p->set_qo[b]);
     char* kd = static_cast<char*>(p->set_k[b]);
     char* vd = static_cast<char*>(p->set_v[b]);
@@ -1087,16 +1144,47 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
     }
     add_stats(st, 0, 0, 0, chunks, 0);
     SA_HIP_RETURN(hipEventRecord(p->set_done[b], cs));
-    {
-      TraceRange range(p->trace, "seqattn:output_d2h");
-      SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->set_done[b], 0));
-      const int32_t rc = copy_rows(oh + (int64_t)kv0 * group * d_bytes, q_pitch, qo, wq, wq, total_q,
-                                   hipMemcpyDeviceToHost, p->d2h);
+    return 0;
+  };
+  auto output_unit = [&](int u) -> int32_t {
+    const int b = u % p->num_sets;
+    int kv0, gk;
+    int64_t wq, wk;
+    unit_heads(u, &kv0, &gk, &wq, &wk);
+    const char* qo = static_cast<const char*>(p->set_qo[b]);
+    char* dst = oh + (int64_t)kv0 * group * d_bytes;
+    TraceRange range(p->trace, "seqattn:output_d2h");
+    SA_HIP_RETURN(hipStreamWaitEvent(p->d2h, p->set_done[b], 0));
+    if (p->staging == nullptr) {
+      const int32_t rc = copy_rows(dst, q_pitch, qo, wq, wq, total_q, hipMemcpyDeviceToHost, p->d2h);
       if (rc != 0) return rc;
-      SA_HIP_RETURN(hipEventRecord(p->set_free[b], p->d2h));
-      p->set_pending[b] = true;
+    } else {
+      // Row chunks through the staging buffer, in order on the D2H stream:
+      // copy a chunk, then scatter it into the host rows with a host
+      // function (run by the runtime when the stream reaches it; the stream
+      // resumes when it returns), then the next chunk.  Nothing here blocks
+      // the calling thread, so later units are enqueued at once.
+      const int64_t rows = p->staging_bytes / wq;
+      for (int64_t r0 = 0; r0 < total_q; r0 += rows) {
+        const int64_t n = std::min(rows, total_q - r0);
+        SA_HIP_RETURN(hipMemcpyAsync(p->staging, qo + r0 * wq, (size_t)(n * wq), hipMemcpyDeviceToHost, p->d2h));
+        scatters.push_back(ScatterRows{dst + r0 * q_pitch, q_pitch, static_cast<const char*>(p->staging), wq, n});
+        SA_HIP_RETURN(hipLaunchHostFunc(p->d2h, scatter_rows, &scatters.back()));
+      }
     }
+    SA_HIP_RETURN(hipEventRecord(p->set_free[b], p->d2h));
+    p->set_pending[b] = true;
     add_stats(st, 0, total_q * wq, 0, 0, 0);
+    return 0;
+  };
+  int next = 0;
+  for (int u = 0; u < units; ++u) {
+    while (next < units && next <= u + p->num_sets - 1) {
+      const int32_t rc = enqueue_unit(next++);
+      if (rc != 0) return rc;
+    }
+    const int32_t rc = output_unit(u);
+    if (rc != 0) return rc;
   }
   // Work the caller enqueues on compute_stream later (a read of the LSE)
   // follows the second stream's launches.
@@ -1673,6 +1761,23 @@ int32_t sa_pipeline_attach_resident_scratch(sa_pipeline* p, void* scratch, int64
   }
   p->vt_scratch = scratch;
   p->vt_scratch_bytes = bytes;
+  return 0;
+}
+
+int32_t sa_pipeline_attach_host_staging(sa_pipeline* p, void* staging, int64_t bytes) {
+  sa::clear_error();
+  if (!p || bytes < 0 || (staging == nullptr) != (bytes == 0)) {
+    sa::set_error("sa_pipeline_attach_host_staging: need a page-locked buffer and its size, or NULL and 0");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (!p->head_groups) {
+    sa::set_error("sa_pipeline_attach_host_staging: only head-group pipelines stage their output");
+    return SA_ERR_BAD_STATE;
+  }
+  // Earlier runs returned only after their copies and scatters finished, so
+  // the previous buffer is no longer read or written.
+  p->staging = staging;
+  p->staging_bytes = bytes;
   return 0;
 }
 

@@ -134,6 +134,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "sa_pipeline_synchronize": (c_int32, [c_void_p]),
     "sa_pipeline_attach_resident_scratch": (c_int32, [c_void_p, c_void_p, c_int64]),
+    "sa_pipeline_attach_host_staging": (c_int32, [c_void_p, c_void_p, c_int64]),
     "sa_pipeline_set_kernel_timing": (c_int32, [c_void_p, c_int32]),
     "sa_pipeline_set_trace_ranges": (c_int32, [c_void_p, c_int32]),
     "sa_pipeline_kernel_timing": (

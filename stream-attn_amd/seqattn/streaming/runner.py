@@ -12,9 +12,10 @@ signatures and validation as the reference.  Additive options:
   inputs): the same Q super-block / K/V chunk schedule then reads them in
   place, nothing crosses PCIe and the output is a device tensor.
 * A plan of the head-group schedule (``schedule="head_groups"``) runs
-  page-locked host inputs into a page-locked host ``out`` with one native
-  call per run, each byte of Q, K and V crossing PCIe once; device outputs
-  and ``run_with_device_output`` need the default schedule.
+  page-locked host inputs into a host ``out`` with one native call per run,
+  each byte of Q, K and V crossing PCIe once (a pageable ``out``, with
+  ``pin_output=False``, is written through 64 MiB of page-locked staging);
+  device outputs and ``run_with_device_output`` need the default schedule.
 """
 
 from __future__ import annotations
@@ -147,11 +148,14 @@ class StreamingAttentionRunner(HipExecutorMixin):
             if out.device.type != "cpu":
                 raise ValueError("schedule='head_groups' returns the output to host memory; "
                                  "a device out needs schedule='q_blocks'")
-            if not all(t.is_pinned() for t in (q_cpu, k_cpu, v_cpu, out)):
+            if not all(t.is_pinned() for t in (q_cpu, k_cpu, v_cpu)):
                 # Strided copies between pageable memory and the device are
                 # staged by the runtime row by row.
                 raise ValueError("schedule='head_groups' copies head columns with strided copies, which need "
-                                 "page-locked q, k, v and out")
+                                 "page-locked q, k and v")
+            # A pageable out (pin_output=False) is written through page-locked
+            # staging by the pipeline.
+            self._workspace.stage_output(not out.is_pinned())
         lse = self._lse_buffer(q_cpu.shape[0], lse_out, return_lse)
         stats = self._prepare_stats(stats)
         started = time.perf_counter()

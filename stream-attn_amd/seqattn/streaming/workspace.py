@@ -28,6 +28,9 @@ from ..planner import AttentionPlan
 
 
 _COPY_STREAMS: dict[int, tuple[torch.cuda.Stream, torch.cuda.Stream]] = {}
+# Page-locked staging of a head-group pipeline's output when the caller's out
+# is pageable (row chunks of up to 64 MiB), outside the device budget.
+HOST_STAGING_BYTES = 64 * 2**20
 # Every workspace with a live native pipeline, so that all of them can be
 # destroyed while the HIP runtime is still up (see close_all_workspaces).
 _LIVE: "weakref.WeakSet[CudaWorkspace]" = weakref.WeakSet()
@@ -83,6 +86,8 @@ class CudaWorkspace:
         self._lib = _native.lib()
         self.plan = plan
         self.resident_scratch: torch.Tensor | None = None
+        self.host_staging: torch.Tensor | None = None
+        self._staging_attached = False
         if plan.schedule == "head_groups":
             self._init_head_groups(plan)
         else:
@@ -211,6 +216,22 @@ class CudaWorkspace:
         self.resident_scratch = scratch
         return needed
 
+    def stage_output(self, enable: bool) -> None:
+        """Head-group pipelines: copy the output through page-locked host
+        staging (for a pageable out; strided copies into pageable memory are
+        staged by the runtime row by row) or straight into the caller's
+        page-locked rows."""
+        if enable == self._staging_attached:
+            return
+        if enable and self.host_staging is None:
+            self.host_staging = torch.empty(HOST_STAGING_BYTES, dtype=torch.uint8, pin_memory=True)
+        buf = self.host_staging if enable else None
+        status = self._lib.sa_pipeline_attach_host_staging(
+            self.handle, None if buf is None else buf.data_ptr(), 0 if buf is None else buf.numel()
+        )
+        _native.check(status, "sa_pipeline_attach_host_staging")
+        self._staging_attached = enable
+
     def release_resident_scratch(self) -> None:
         """Detach and drop the transposed-V scratch.  Runs already enqueued
         still read it: the buffer was allocated on the compute stream, so
@@ -232,6 +253,7 @@ class CudaWorkspace:
             self._lib.sa_pipeline_destroy(handle)
             self.handle = None
         self.resident_scratch = None
+        self.host_staging = None
         _LIVE.discard(self)
 
     def __del__(self) -> None:

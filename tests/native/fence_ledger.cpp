@@ -169,6 +169,14 @@ hipError_t hipMemcpy2DAsync(void* dst, size_t dpitch, const void* src, size_t sp
   return hipSuccess;
 }
 
+// A host function is an operation of its stream with no device ranges; it
+// runs here at once (the tests that enqueue one give it real host memory).
+hipError_t hipLaunchHostFunc(hipStream_t stream, hipHostFn_t fn, void* user_data) {
+  push(Op{kKernel, stream_id(stream), -1, {}, {}, "host function"});
+  fn(user_data);
+  return hipSuccess;
+}
+
 // ------------------------------------------------------- kernel launchers
 namespace sa {
 

@@ -397,3 +397,63 @@ def test_step_api_is_refused_on_head_group_pipelines(ledger):
     assert ledger.sa_pipeline_finalize(handle, 0, 16, None, 0, 0, 0xC0FFEE) == -4
     assert ledger.sa_pipeline_release_q(handle, 0xC0FFEE) == -4
     assert ledger.sa_pipeline_destroy(handle) == 0
+
+
+def test_head_group_schedule_with_host_staging_is_race_free(ledger):
+    # A pageable output goes through page-locked staging in row chunks: on
+    # the D2H stream a chunk's copy, then a host function scattering it into
+    # the host rows (the staging and the output are real host memory here:
+    # the scatter runs).  The ledger checks the device-side order: each set's
+    # next copies after its output left, each staging copy after the unit's
+    # launches and after the previous chunk's scatter.
+    import numpy as np
+
+    q_heads, kv_heads, head_dim = 4, 4, 64
+    q_lengths, k_lengths = [1500, 900], [1200, 900]
+    tq = sum(q_lengths)
+    row = q_heads * head_dim * HEAD_BYTES
+    staging = np.zeros(8192, dtype=np.uint8)  # 64 output rows of one head
+    out = np.zeros(tq * row, dtype=np.uint8)
+    dev = Space(0x7000_0000_0000)
+    host = Space(0x5000_0000_0000)
+    cu_q, q_b = bounds(q_lengths)
+    cu_k, k_b = bounds(k_lengths)
+    for num_sets in (1, 2):
+        ledger.ledger_reset()
+        qo = [dev.take(tq * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+        ks = [dev.take(k_b[-1] * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+        vs = [dev.take(k_b[-1] * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+        handle = ctypes.c_void_p()
+        assert ledger.sa_pipeline_create_head_groups(
+            ctypes.byref(handle), 0, (ctypes.c_void_p * 2)(*qo), (ctypes.c_void_p * 2)(*ks),
+            (ctypes.c_void_p * 2)(*vs), None, 0, num_sets, tq, k_b[-1], 1, 256, q_heads, kv_heads, head_dim, 0, None,
+            None) == 0
+        assert ledger.sa_pipeline_attach_host_staging(handle, staging.ctypes.data, staging.nbytes) == 0
+        q_host, k_host, v_host = host.take(tq * row), host.take(k_b[-1] * row), host.take(k_b[-1] * row)
+        stats = _native.PipelineStats()
+        status = ledger.sa_pipeline_run(handle, q_host, k_host, v_host, out.ctypes.data, None, 0, cu_q, cu_k, 2,
+                                        0.125, 0, 0xC0FFEE, ctypes.byref(stats))
+        assert status == 0, ledger.sa_last_error()
+        assert stats.d2h_bytes == tq * row
+        counts = (ctypes.c_int64 * 4)()
+        ledger.ledger_counts(counts)
+        chunks = 4 * -(-tq // 64)  # per unit one staging copy and one scatter per 64-row chunk
+        assert counts[1] == chunks
+        assert counts[2] == 4 * 2 + chunks  # update launches per unit and segment, and the scatters
+        check(ledger, f"head groups with host staging, sets={num_sets}")
+        assert ledger.sa_pipeline_destroy(handle) == 0
+    # Staging smaller than one output row is refused before anything runs.
+    handle = ctypes.c_void_p()
+    bufs = (ctypes.c_void_p * 2)(dev.take(1 << 20), dev.take(1 << 20))
+    assert ledger.sa_pipeline_create_head_groups(ctypes.byref(handle), 0, bufs, bufs, bufs, None, 0, 1, 1024, 1024, 4,
+                                                 256, 64, 4, 256, 0, None, None) == 0
+    assert ledger.sa_pipeline_attach_host_staging(handle, staging.ctypes.data, staging.nbytes) == 0
+    ledger.ledger_reset()
+    cu = (ctypes.c_int64 * 2)(0, 512)
+    assert ledger.sa_pipeline_run(handle, 0x5000_0000_0000, 0x5100_0000_0000, 0x5200_0000_0000, out.ctypes.data, None,
+                                  0, cu, cu, 1, 0.1, 0, 0xC0FFEE, None) == -1
+    assert b"host staging" in ledger.sa_last_error()
+    counts = (ctypes.c_int64 * 4)()
+    ledger.ledger_counts(counts)
+    assert list(counts) == [0, 0, 0, 0]
+    assert ledger.sa_pipeline_destroy(handle) == 0

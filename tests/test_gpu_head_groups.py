@@ -153,3 +153,37 @@ def test_head_groups_device_inputs_and_unsupported_outputs():
     torch.testing.assert_close(lse_d.cpu(), lse.cpu(), atol=0, rtol=0)
     ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=800, kv_chunk=256, causal=True)
     check(out, lse, ref_o, ref_l)
+
+
+@pytest.mark.parametrize("sets", [1, 2])
+def test_head_groups_pageable_output_through_staging(sets):
+    """A pageable out (pin_output=False) is written through the pipeline's
+    page-locked staging in row chunks, bit-identical to a page-locked out;
+    GQA, two segments, causal."""
+    announce(f"head groups pageable output sets={sets}")
+    gen = torch.Generator().manual_seed(79)
+    q = pinned_randn((3000, 8, 128), torch.bfloat16, gen)
+    k = pinned_randn((2800, 4, 128), torch.bfloat16, gen)
+    v = pinned_randn((2800, 4, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 1000, 3000], dtype=torch.int32)
+    cu_k = torch.tensor([0, 900, 2800], dtype=torch.int32)
+    base = StreamingAttentionConfig(backend="hip", kv_chunk_tokens=512, schedule="head_groups")
+    plan = build_plan(q_heads=8, kv_heads=4, head_dim=128, dtype=torch.bfloat16, device="cuda",
+                      max_q_tokens=3000, max_kv_tokens=2800, config=base)
+    plan = dataclasses.replace(plan, head_group_kv_heads=1, head_group_sets=sets,
+                               head_group_vt_bytes=128 * 2816 * 2)
+    results = []
+    for pinned in (True, False):
+        config = dataclasses.replace(base, pin_output=pinned)
+        runner = StreamingAttentionRunner(plan, config)
+        out = torch.empty(q.shape, dtype=q.dtype, pin_memory=pinned)
+        try:
+            lse = runner(q, k, v, cu_q, cu_k, causal=True, out=out, return_lse=True)[1]
+        finally:
+            runner.close()
+        assert out.is_pinned() == pinned
+        results.append((out, lse))
+    torch.testing.assert_close(results[1][0], results[0][0], atol=0, rtol=0)
+    torch.testing.assert_close(results[1][1], results[0][1], atol=0, rtol=0)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=3000, kv_chunk=512, causal=True)
+    check(results[1][0], results[1][1], ref_o, ref_l)
