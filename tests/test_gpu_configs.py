@@ -172,17 +172,18 @@ def test_config5_1m_64h_peaked_keys_8gib_workspace():
                  f"{rows.size} rows x {h} heads")
 
 
+@pytest.mark.parametrize("schedule", ["q_blocks", "head_groups"])
 @pytest.mark.parametrize("causal", [True, False])
-def test_dense_and_varlen_api_wrappers_on_the_hip_path(causal):
+def test_dense_and_varlen_api_wrappers_on_the_hip_path(causal, schedule):
     # The reference's tests/test_api.py:7-25 shapes (batch 2, 7 queries,
     # 9 keys, 4 query heads over 2 K/V heads, d 32, q chunk 3, kv chunk 4),
-    # in bf16 on the HIP path, against the oracle.
-    announce(f"API wrappers causal={causal}")
+    # in bf16 on the HIP path, against the oracle; in both schedules.
+    announce(f"API wrappers causal={causal} schedule={schedule}")
     torch.manual_seed(11)
     q = torch.randn(2, 7, 4, 32).to(torch.bfloat16)
     k = torch.randn(2, 9, 2, 32).to(torch.bfloat16)
     v = torch.randn_like(k.float()).to(torch.bfloat16)
-    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=3, kv_chunk_tokens=4)
+    config = StreamingAttentionConfig(backend="hip", q_chunk_tokens=3, kv_chunk_tokens=4, schedule=schedule)
     dense = streaming_attn_func(q.pin_memory(), k.pin_memory(), v.pin_memory(), causal=causal, config=config)
     assert dense.shape == q.shape and dense.dtype == q.dtype and dense.device.type == "cpu"
     cu_q = torch.tensor([0, 7, 14], dtype=torch.int32)
