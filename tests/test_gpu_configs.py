@@ -168,8 +168,29 @@ def test_config5_1m_64h_peaked_keys_8gib_workspace():
     rows = signature_and_random_rows(n, 1024, seed=5)
     ref_o, ref_l = oracle_rows(q, k, v, rows, kv_chunk=8192)
     idx = torch.from_numpy(rows)
-    check_parity(out[idx].float().numpy(), lse[:, idx.cuda()].cpu().numpy(), ref_o, ref_l,
-                 f"{rows.size} rows x {h} heads")
+    o_rows, l_rows = out[idx].clone(), lse[:, idx.cuda()].cpu()
+    check_parity(o_rows.float().numpy(), l_rows.numpy(), ref_o, ref_l, f"{rows.size} rows x {h} heads")
+    # The same step in the head-group schedule (22 units of 3 K/V heads; a
+    # pageable output goes through the pipeline's page-locked staging):
+    # the same bits on the sampled rows.
+    hg_config = StreamingAttentionConfig(workspace_budget_bytes=8 * 2**30, kv_chunk_tokens=8192, backend="hip",
+                                         pin_output=out.is_pinned(), schedule="head_groups")
+    hg_plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
+                         max_q_tokens=n, max_kv_tokens=n, config=hg_config)
+    assert (hg_plan.head_group_sets, hg_plan.head_group_kv_heads, hg_plan.head_group_units) == (2, 3, 22)
+    runner = StreamingAttentionRunner(hg_plan, hg_config)
+    out.fill_(float("nan"))
+    lse.fill_(float("nan"))
+    hg_stats = StreamingAttentionStats()
+    try:
+        runner(q, k, v, cu, cu, out=out, lse_out=lse, stats=hg_stats)
+        torch.cuda.synchronize()
+    finally:
+        runner.close()
+    print(f"    head groups: {hg_stats.wall_seconds:.2f} s, H2D {hg_stats.h2d_bytes / 1e9:.1f} GB", flush=True)
+    assert hg_stats.h2d_bytes == 3 * n * h * d * 2
+    torch.testing.assert_close(out[idx], o_rows, atol=0, rtol=0)
+    torch.testing.assert_close(lse[:, idx.cuda()].cpu(), l_rows, atol=0, rtol=0)
 
 
 @pytest.mark.parametrize("schedule", ["q_blocks", "head_groups"])
