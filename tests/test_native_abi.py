@@ -63,6 +63,26 @@ def test_resident_scratch_attach_rejects_bad_arguments_without_a_gpu():
     assert b"sa_pipeline_attach_resident_scratch" in lib.sa_last_error()
 
 
+@pytest.mark.skipif(not _native.library_is_built(), reason="native library not built")
+def test_head_group_pipeline_rejects_bad_plans_without_a_gpu():
+    import ctypes
+
+    lib = _native.lib()
+    handle = ctypes.c_void_p()
+    bufs = (ctypes.c_void_p * 2)(16, 32)
+    # num_sets 3 (at most 2), then a group of 5 K/V heads out of 4, then a
+    # misaligned buffer: rejected before any HIP call.
+    for sets, group, q_buf in ((3, 1, bufs), (1, 5, bufs), (1, 1, (ctypes.c_void_p * 2)(17, 32))):
+        status = lib.sa_pipeline_create_head_groups(ctypes.byref(handle), 0, q_buf, bufs, bufs, None, 0, sets, 64, 64,
+                                                    group, 64, 8, 4, 128, 0, None, None)
+        assert status == -1, (sets, group)
+        assert b"sa_pipeline_create_head_groups" in lib.sa_last_error()
+        assert not handle.value
+    assert lib.sa_pipeline_create_head_groups(ctypes.byref(handle), 0, bufs, bufs, bufs, None, 0, 1, 64, 64, 1, 64, 8,
+                                              4, 128, 9, None, None) == -2  # dtype
+    assert lib.sa_pipeline_attach_host_staging(None, None, 0) == -1
+
+
 def test_backend_resolution_never_falls_back_to_cpu():
     with pytest.raises(ValueError, match="not part of this package"):
         resolve_backend("reference", torch.bfloat16, torch.device("cpu"))
