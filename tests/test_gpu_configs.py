@@ -151,8 +151,9 @@ def test_config5_1m_64h_peaked_keys_8gib_workspace():
         out = torch.empty((n, h, d), dtype=torch.bfloat16)
     warnings.warn(RunModeNotice(
         "config 5 wrote its output to page-locked host memory" if out.is_pinned() else
-        f"config 5 wrote its output to PAGEABLE host memory (page-locking 16 GiB failed: {refused}); its copies "
-        "went through the runtime's staging"))
+        f"config 5 wrote its output to PAGEABLE host memory (page-locking 16 GiB failed: {refused}); the Q-block "
+        "run's copies went through the runtime's staging, the head-group run's through the pipeline's page-locked "
+        "staging"))
     config = StreamingAttentionConfig(workspace_budget_bytes=8 * 2**30, kv_chunk_tokens=8192, backend="hip",
                                       pin_output=out.is_pinned())
     plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
