@@ -282,6 +282,26 @@ int32_t sa_pipeline_run(
     void* compute_stream, sa_pipeline_stats* stats);
 
 /*
+ * Head-group pipelines only: sa_pipeline_run with the output in device
+ * memory.  out [total_q_tokens, q_heads, head_dim] dtype with strides
+ * (stride_ot, stride_oh, 1), 16-byte aligned, strides multiples of 8; each
+ * unit's fused launches write the rows of its heads straight into it, and no
+ * output copy is made.  Enqueued on compute_stream (and the pipeline's
+ * second stream, joined back into it); returns once the host inputs have
+ * been copied, before the launches end: later work on compute_stream sees
+ * the output and the LSE.  No counterpart in the reference (its device
+ * outputs go through output_transform, executor.py:145-172).
+ */
+int32_t sa_pipeline_run_device_output(
+    sa_pipeline* pipeline,
+    const void* q_host, const void* k_host, const void* v_host,
+    void* out, int64_t stride_ot, int64_t stride_oh,
+    float* lse, int64_t lse_stride_h,
+    const int64_t* cu_seqlens_q, const int64_t* cu_seqlens_k, int32_t num_segments,
+    double softmax_scale, int32_t causal,
+    void* compute_stream, sa_pipeline_stats* stats);
+
+/*
  * Step interface used by device-consumer mode (reference executor.py:44-186
  * with output_transform): the caller runs one Q super-block at a time and may
  * consume the finalized device tile between finalize and D2H.  sa_pipeline_run

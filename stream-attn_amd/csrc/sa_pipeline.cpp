@@ -1033,7 +1033,8 @@ void scatter_rows(void* arg) {
 // host function once its copy has landed, while later units' launches run.
 int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const char* vh, char* oh, float* lse,
                         int64_t lse_sh, const int64_t* cu_q, const int64_t* cu_k, int32_t num_segments,
-                        double scale, int32_t causal, hipStream_t compute, sa_pipeline_stats* st) {
+                        double scale, int32_t causal, hipStream_t compute, sa_pipeline_stats* st,
+                        char* out_dev = nullptr, int64_t so_t = 0, int64_t so_h = 0) {
   for (int32_t s = 0; s < num_segments; ++s) {
     const int64_t q_length = cu_q[s + 1] - cu_q[s], k_length = cu_k[s + 1] - cu_k[s];
     if (cu_q[s] < 0 || cu_k[s] < 0 || q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0) ||
@@ -1132,8 +1133,13 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
                                                   p->head_dim, p->set_vt[b], t_pad, cs);
         if (rc != 0) return rc;
       }
-      const sa::FusedOutput fused{qo + q_start * wq, (int64_t)gq * p->head_dim, p->head_dim,
-                                  lse ? lse + (int64_t)kv0 * group * lse_sh : nullptr, lse_sh, q_start};
+      // The output goes over the unit's Q rows (copied out afterwards), or
+      // straight into the caller's device rows of the unit's heads.
+      const sa::FusedOutput fused =
+          out_dev ? sa::FusedOutput{out_dev + (q_start * so_t + (int64_t)kv0 * group * so_h) * 2, so_t, so_h,
+                                    lse ? lse + (int64_t)kv0 * group * lse_sh : nullptr, lse_sh, q_start}
+                  : sa::FusedOutput{qo + q_start * wq, (int64_t)gq * p->head_dim, p->head_dim,
+                                    lse ? lse + (int64_t)kv0 * group * lse_sh : nullptr, lse_sh, q_start};
       const int32_t rc = launch_unit(p, qo + q_start * wq, (int64_t)gq * p->head_dim, kd + k_start * wk,
                                      (int64_t)gk * p->head_dim, vt ? static_cast<const char*>(p->set_vt[b]) : vseg,
                                      vt ? t_pad : (int64_t)gk * p->head_dim, vt ? 128 * t_pad : p->head_dim,
@@ -1151,6 +1157,12 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
     int kv0, gk;
     int64_t wq, wk;
     unit_heads(u, &kv0, &gk, &wq, &wk);
+    if (out_dev != nullptr) {
+      // The launches wrote the caller's rows: the set is free once they end.
+      SA_HIP_RETURN(hipEventRecord(p->set_free[b], streams[b]));
+      p->set_pending[b] = true;
+      return 0;
+    }
     const char* qo = static_cast<const char*>(p->set_qo[b]);
     char* dst = oh + (int64_t)kv0 * group * d_bytes;
     TraceRange range(p->trace, "seqattn:output_d2h");
@@ -1186,10 +1198,16 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
     const int32_t rc = output_unit(u);
     if (rc != 0) return rc;
   }
-  // Work the caller enqueues on compute_stream later (a read of the LSE)
-  // follows the second stream's launches.
+  // Work the caller enqueues on compute_stream later (a read of the LSE or
+  // of a device output) follows the second stream's launches.
   const int32_t jrc = join.finish();
   if (jrc != 0) return jrc;
+  if (out_dev != nullptr) {
+    // The host inputs are no longer read once the last copies have landed;
+    // the launches complete in stream order on compute_stream.
+    SA_HIP_RETURN(hipStreamSynchronize(p->h2d));
+    return 0;
+  }
   SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
   return 0;
 }
@@ -1853,6 +1871,36 @@ void* sa_pipeline_output_slot(sa_pipeline* p, int32_t index) {
 }
 
 void* sa_pipeline_q_buffer(sa_pipeline* p) { return p ? p->q_buffer : nullptr; }
+
+int32_t sa_pipeline_run_device_output(sa_pipeline* p, const void* q_host, const void* k_host, const void* v_host,
+                                      void* out, int64_t stride_ot, int64_t stride_oh, float* lse,
+                                      int64_t lse_stride_h, const int64_t* cu_seqlens_q,
+                                      const int64_t* cu_seqlens_k, int32_t num_segments, double softmax_scale,
+                                      int32_t causal, void* compute_stream, sa_pipeline_stats* stats) {
+  sa::clear_error();
+  if (!p || !q_host || !k_host || !v_host || !out || !cu_seqlens_q || !cu_seqlens_k || num_segments < 0) {
+    sa::set_error("sa_pipeline_run_device_output: null argument");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  if (!p->head_groups) {
+    sa::set_error("sa_pipeline_run_device_output: only head-group pipelines write a device output from their "
+                  "launches (token-block pipelines use the step API)");
+    return SA_ERR_BAD_STATE;
+  }
+  // The fused launches' output rules, checked before anything is enqueued.
+  if (stride_ot % 8 != 0 || stride_oh % 8 != 0 || stride_oh < p->head_dim ||
+      stride_ot < (int64_t)p->q_heads * stride_oh || reinterpret_cast<uintptr_t>(out) % 16 != 0) {
+    sa::set_error("sa_pipeline_run_device_output: out must be 16-byte aligned with strides that are multiples of "
+                  "8 and hold [tokens, q_heads, head_dim]");
+    return SA_ERR_INVALID_ARGUMENT;
+  }
+  sa::DeviceGuard guard(p->device);
+  SA_HIP_RETURN(guard.status());
+  return run_head_groups(p, static_cast<const char*>(q_host), static_cast<const char*>(k_host),
+                         static_cast<const char*>(v_host), nullptr, lse, lse_stride_h, cu_seqlens_q, cu_seqlens_k,
+                         num_segments, softmax_scale, causal, static_cast<hipStream_t>(compute_stream), stats,
+                         static_cast<char*>(out), stride_ot, stride_oh);
+}
 
 int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, const void* v_host,
                         void* out_host, float* lse, int64_t lse_stride_h,

@@ -80,6 +80,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          ctypes.POINTER(c_int64), ctypes.POINTER(c_int64), c_int32, c_double, c_int32,
          c_void_p, ctypes.POINTER(PipelineStats)],
     ),
+    "sa_pipeline_run_device_output": (
+        c_int32,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+         ctypes.POINTER(c_int64), ctypes.POINTER(c_int64), c_int32, c_double, c_int32,
+         c_void_p, ctypes.POINTER(PipelineStats)],
+    ),
     "sa_pipeline_load_q": (
         c_int32, [c_void_p, c_void_p, c_int32, c_void_p, ctypes.POINTER(PipelineStats)]
     ),

@@ -80,6 +80,47 @@ class HipExecutorMixin:
         _merge_stats(stats, native_stats)
         return out
 
+    def _run_native_device_output(
+        self,
+        q_cpu: torch.Tensor,
+        k_cpu: torch.Tensor,
+        v_cpu: torch.Tensor,
+        q_bounds: list[int],
+        k_bounds: list[int],
+        scale: float,
+        causal: bool,
+        out: torch.Tensor,
+        stats: StreamingAttentionStats,
+        lse: torch.Tensor | None = None,
+    ) -> torch.Tensor:
+        """Head-group schedule into a device ``out``: the unit launches write
+        its rows directly (one native call, no output copy).  Ordered after
+        the work the caller's current stream has enqueued so far, and the
+        caller's stream waits for it in turn, as for HBM-resident inputs."""
+        workspace = self._workspace
+        self._check_lse(lse, q_cpu.shape[0])
+        native_stats = _native.PipelineStats()
+        compute = workspace.compute_stream
+        with torch.cuda.device(self.plan.device):
+            caller = torch.cuda.current_stream()
+            if caller != compute:
+                compute.wait_stream(caller)
+        with torch.cuda.device(self.plan.device), self._range("seqattn:run"):
+            status = _native.lib().sa_pipeline_run_device_output(
+                workspace.handle,
+                q_cpu.data_ptr(), k_cpu.data_ptr(), v_cpu.data_ptr(),
+                out.data_ptr(), out.stride(0), out.stride(1),
+                None if lse is None else lse.data_ptr(), 0 if lse is None else lse.stride(0),
+                _bounds_array(q_bounds), _bounds_array(k_bounds), len(q_bounds) - 1,
+                float(scale), int(bool(causal)),
+                compute.cuda_stream, ctypes.byref(native_stats),
+            )
+        _native.check(status, "sa_pipeline_run_device_output")
+        if caller != compute:
+            caller.wait_stream(compute)
+        _merge_stats(stats, native_stats)
+        return out
+
     def _run_resident(
         self,
         q: torch.Tensor,

@@ -12,10 +12,11 @@ signatures and validation as the reference.  Additive options:
   inputs): the same Q super-block / K/V chunk schedule then reads them in
   place, nothing crosses PCIe and the output is a device tensor.
 * A plan of the head-group schedule (``schedule="head_groups"``) runs
-  page-locked host inputs into a host ``out`` with one native call per run,
-  each byte of Q, K and V crossing PCIe once (a pageable ``out``, with
-  ``pin_output=False``, is written through 64 MiB of page-locked staging);
-  device outputs and ``run_with_device_output`` need the default schedule.
+  page-locked host inputs with one native call per run, each byte of Q, K
+  and V crossing PCIe once, into a host ``out`` (a pageable one, with
+  ``pin_output=False``, is written through 64 MiB of page-locked staging) or
+  a device ``out`` (written by the launches, no output copy);
+  ``run_with_device_output`` needs the default schedule.
 """
 
 from __future__ import annotations
@@ -145,9 +146,8 @@ class StreamingAttentionRunner(HipExecutorMixin):
             raise ValueError("out must be a CPU tensor matching q shape and dtype")
         self._prepare_io(q_cpu, k_cpu, v_cpu, out)
         if self.plan.schedule == "head_groups":
-            if out.device.type != "cpu":
-                raise ValueError("schedule='head_groups' returns the output to host memory; "
-                                 "a device out needs schedule='q_blocks'")
+            if out.device.type != "cpu" and (out.device != self._device() or out.stride(2) != 1):
+                raise ValueError("a device out must be on the plan's device with unit stride over head_dim")
             if not all(t.is_pinned() for t in (q_cpu, k_cpu, v_cpu)):
                 # Strided copies between pageable memory and the device are
                 # staged by the runtime row by row.
@@ -155,12 +155,15 @@ class StreamingAttentionRunner(HipExecutorMixin):
                                  "page-locked q, k and v")
             # A pageable out (pin_output=False) is written through page-locked
             # staging by the pipeline.
-            self._workspace.stage_output(not out.is_pinned())
+            self._workspace.stage_output(out.device.type == "cpu" and not out.is_pinned())
         lse = self._lse_buffer(q_cpu.shape[0], lse_out, return_lse)
         stats = self._prepare_stats(stats)
         started = time.perf_counter()
         if out.device.type == "cpu":
             result = self._run_native(q_cpu, k_cpu, v_cpu, q_bounds, k_bounds, scale, causal, out, stats, lse)
+        elif self.plan.schedule == "head_groups":
+            result = self._run_native_device_output(q_cpu, k_cpu, v_cpu, q_bounds, k_bounds, scale, causal, out,
+                                                    stats, lse)
         else:
             result = self._run_steps(q_cpu, k_cpu, v_cpu, q_bounds, k_bounds, scale, causal, out, stats, lse=lse)
         stats.wall_seconds += time.perf_counter() - started

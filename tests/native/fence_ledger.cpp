@@ -32,8 +32,11 @@
 
 namespace {
 
+// [lo, hi), or with pitch > 0 the rows [lo + i * pitch, lo + i * pitch +
+// width) that start below hi.
 struct Range {
-  uintptr_t lo, hi;  // [lo, hi)
+  uintptr_t lo, hi;
+  uintptr_t pitch = 0, width = 0;
 };
 
 enum Kind { kCopyH2D, kCopyD2H, kCopyD2D, kKernel, kRecord, kWait, kStreamSync, kEventSync };
@@ -82,10 +85,41 @@ Range span(const void* p, int64_t bytes) {
   return Range{lo, lo + (uintptr_t)std::max<int64_t>(bytes, 0)};
 }
 
+// Rows of `width` bytes, `pitch` apart (`count` of them), from p.
+Range strided(const void* p, int64_t width, int64_t pitch, int64_t count) {
+  const uintptr_t lo = reinterpret_cast<uintptr_t>(p);
+  if (count <= 0 || width <= 0) return Range{lo, lo};
+  if (count == 1 || width >= pitch) return Range{lo, lo + (uintptr_t)((count - 1) * pitch + width)};
+  return Range{lo, lo + (uintptr_t)((count - 1) * pitch + width), (uintptr_t)pitch, (uintptr_t)width};
+}
+
+// Whether a row range and a contiguous range [a, b) share a byte: some row
+// start s = lo + i * pitch with a - width < s < b.
+bool rows_meet(const Range& r, uintptr_t a, uintptr_t b) {
+  const uintptr_t first = a + 1 > r.lo + r.width ? (a + 1 - r.width - r.lo + r.pitch - 1) / r.pitch : 0;
+  const uintptr_t s = r.lo + first * r.pitch;
+  return s < b && s < r.hi;
+}
+
+bool intersect(const Range& x, const Range& y) {
+  if (!(x.lo < y.hi && y.lo < x.hi && x.lo < x.hi && y.lo < y.hi)) return false;
+  if (!x.pitch && !y.pitch) return true;
+  if (!x.pitch) return rows_meet(y, x.lo, x.hi);
+  if (!y.pitch) return rows_meet(x, y.lo, y.hi);
+  if (x.pitch != y.pitch) return true;  // different pitches: the bounding ranges decide
+  // Same pitch, overlapping extents: the column windows must meet.
+  const uintptr_t p = x.pitch, cx = x.lo % p, cy = y.lo % p;
+  for (const uintptr_t shift : {(uintptr_t)0, p}) {
+    if (cx < cy + shift + y.width && cy + shift < cx + x.width) return true;
+    if (cy < cx + shift + x.width && cx + shift < cy + y.width) return true;
+  }
+  return false;
+}
+
 bool overlaps(const std::vector<Range>& a, const std::vector<Range>& b) {
   for (const Range& x : a)
     for (const Range& y : b)
-      if (x.lo < y.hi && y.lo < x.hi && x.lo < x.hi && y.lo < y.hi) return true;
+      if (intersect(x, y)) return true;
   return false;
 }
 
@@ -157,14 +191,12 @@ hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKin
   return hipSuccess;
 }
 
-// A strided copy is recorded by the bounding range of its rows on each side:
-// the gaps between rows count as accessed, which can only add conflicts.
+// A strided copy reads and writes rows of `width` bytes on each side.
 hipError_t hipMemcpy2DAsync(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height,
                             hipMemcpyKind kind, hipStream_t stream) {
   const Kind k = kind == hipMemcpyHostToDevice ? kCopyH2D : kind == hipMemcpyDeviceToHost ? kCopyD2H : kCopyD2D;
-  const int64_t src_bytes = height ? (int64_t)((height - 1) * spitch + width) : 0;
-  const int64_t dst_bytes = height ? (int64_t)((height - 1) * dpitch + width) : 0;
-  push(Op{k, stream_id(stream), -1, {span(src, src_bytes)}, {span(dst, dst_bytes)},
+  push(Op{k, stream_id(stream), -1, {strided(src, (int64_t)width, (int64_t)spitch, (int64_t)height)},
+          {strided(dst, (int64_t)width, (int64_t)dpitch, (int64_t)height)},
           k == kCopyH2D ? "h2d 2-d copy" : k == kCopyD2H ? "d2h 2-d copy" : "d2d 2-d copy"});
   return hipSuccess;
 }
@@ -189,7 +221,7 @@ int32_t update_block_rows(int32_t head_dim) {
 int32_t launch_update(const void* q, const void* k, const void* v, float* m, float* l, float* acc, int64_t sq_t,
                       int64_t, int64_t sk_t, int64_t, int64_t sv_t, int64_t sv_h, int64_t ss_t, int64_t,
                       int64_t sa_t, int64_t, int32_t q_tokens, int32_t kv_tokens, int32_t q_heads,
-                      int32_t kv_heads, int32_t, int32_t, int32_t, int32_t, double, int32_t flags, int32_t,
+                      int32_t kv_heads, int32_t head_dim, int32_t, int32_t, int32_t, double, int32_t flags, int32_t,
                       hipStream_t stream, int32_t, const FusedOutput* fused, bool v_transposed, bool tiled) {
   Op op{kKernel, stream_id(stream), -1, {}, {}, "update"};
   op.reads.push_back(rows_of(q, q_tokens, sq_t, 2));
@@ -204,7 +236,10 @@ int32_t launch_update(const void* q, const void* k, const void* v, float* m, flo
   }
   if (!(flags & SA_FLAG_INITIALIZE)) op.reads.insert(op.reads.end(), state.begin(), state.end());
   if (fused) {
-    op.writes.push_back(rows_of(fused->out, q_tokens, fused->so_t, 2));
+    // Each head's output columns of every row.
+    for (int h = 0; h < q_heads; ++h)
+      op.writes.push_back(strided(static_cast<const char*>(fused->out) + h * fused->so_h * 2, head_dim * 2,
+                                  fused->so_t * 2, q_tokens));
     lse_ranges(op.writes, fused->lse, fused->lse_sh, fused->lse_off, q_tokens, q_heads);
   } else {
     op.writes = state;

@@ -457,3 +457,46 @@ def test_head_group_schedule_with_host_staging_is_race_free(ledger):
     ledger.ledger_counts(counts)
     assert list(counts) == [0, 0, 0, 0]
     assert ledger.sa_pipeline_destroy(handle) == 0
+
+
+@pytest.mark.parametrize("num_sets", [1, 2])
+def test_head_group_schedule_into_device_output_is_race_free(ledger, num_sets):
+    # The unit launches write the caller's device rows of their heads; no
+    # output copy.  A set's next copies wait for its launches, and the
+    # call returns after the last input copy landed.
+    q_heads, kv_heads, head_dim = 6, 3, 64
+    q_lengths, k_lengths = [1500, 0, 900], [1200, 40, 900]
+    dev = Space(0x7000_0000_0000)
+    host = Space(0x5000_0000_0000)
+    cu_q, q_b = bounds(q_lengths)
+    cu_k, k_b = bounds(k_lengths)
+    tq, tk = q_b[-1], k_b[-1]
+    qo = [dev.take(tq * 2 * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+    ks = [dev.take(tk * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+    vs = [dev.take(tk * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+    ledger.ledger_reset()
+    handle = ctypes.c_void_p()
+    assert ledger.sa_pipeline_create_head_groups(
+        ctypes.byref(handle), 0, (ctypes.c_void_p * 2)(*qo), (ctypes.c_void_p * 2)(*ks), (ctypes.c_void_p * 2)(*vs),
+        None, 0, num_sets, tq, tk, 1, 256, q_heads, kv_heads, head_dim, 0, None, None) == 0
+    row = q_heads * head_dim * HEAD_BYTES
+    q_host, k_host = host.take(tq * row), host.take(tk * kv_heads * head_dim * HEAD_BYTES)
+    v_host = host.take(tk * kv_heads * head_dim * HEAD_BYTES)
+    out = dev.take(tq * row)
+    lse = dev.take(q_heads * tq * 4)
+    stats = _native.PipelineStats()
+    status = ledger.sa_pipeline_run_device_output(handle, q_host, k_host, v_host, out, q_heads * head_dim, head_dim,
+                                                  lse, tq, cu_q, cu_k, 3, 0.125, 1, 0xC0FFEE, ctypes.byref(stats))
+    assert status == 0, ledger.sa_last_error()
+    assert stats.d2h_bytes == 0
+    counts = (ctypes.c_int64 * 4)()
+    ledger.ledger_counts(counts)
+    assert counts[1] == 0 and counts[2] == 3 * 2
+    check(ledger, f"head groups into device output, sets={num_sets}")
+    # misaligned output strides are refused before anything is enqueued
+    ledger.ledger_reset()
+    assert ledger.sa_pipeline_run_device_output(handle, q_host, k_host, v_host, out, q_heads * head_dim + 4,
+                                                head_dim, None, 0, cu_q, cu_k, 3, 0.125, 0, 0xC0FFEE, None) == -1
+    ledger.ledger_counts(counts)
+    assert list(counts) == [0, 0, 0, 0]
+    assert ledger.sa_pipeline_destroy(handle) == 0

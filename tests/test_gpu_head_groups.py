@@ -123,10 +123,11 @@ def test_head_groups_repeated_runs_reuse_the_sets():
     check(small[0], small[1], ref_o, ref_l)
 
 
-def test_head_groups_device_inputs_and_unsupported_outputs():
-    """Device-resident inputs run the fused launch on a head-group runner
-    (bit-identical to its host run); device outputs and consumers are refused
-    before anything runs."""
+def test_head_groups_device_inputs_device_output_and_consumers():
+    """On a head-group runner: device-resident inputs run the fused launch,
+    and a device out is written by the unit launches (no output copy), both
+    bit-identical to the host run; device consumers are refused before
+    anything runs."""
     announce("head groups device inputs")
     gen = torch.Generator().manual_seed(73)
     q = pinned_randn((800, 4, 128), torch.bfloat16, gen)
@@ -141,9 +142,13 @@ def test_head_groups_device_inputs_and_unsupported_outputs():
     try:
         out, lse = runner(q, k, v, cu_q, cu_k, causal=True, return_lse=True)
         out_d, lse_d = runner(q.cuda(), k.cuda(), v.cuda(), cu_q, cu_k, causal=True, return_lse=True)
+        dev_out = torch.full(q.shape, float("nan"), dtype=q.dtype, device="cuda")
+        stats = StreamingAttentionStats()
+        _, lse_o = runner(q, k, v, cu_q, cu_k, causal=True, out=dev_out, return_lse=True, stats=stats)
         torch.cuda.synchronize()
-        with pytest.raises(ValueError, match="head_groups"):
-            runner(q, k, v, cu_q, cu_k, out=torch.empty(q.shape, dtype=q.dtype, device="cuda"))
+        assert stats.d2h_bytes == 0 and stats.h2d_bytes == (q.numel() + k.numel() + v.numel()) * 2
+        torch.testing.assert_close(dev_out.cpu(), out, atol=0, rtol=0)
+        torch.testing.assert_close(lse_o.cpu(), lse.cpu(), atol=0, rtol=0)
         with pytest.raises(ValueError, match="q_blocks"):
             runner.run_with_device_output(q, k, v, cu_q, cu_k, output_transform=None,
                                           out=torch.empty(q.shape, dtype=q.dtype, device="cuda"))
