@@ -15,9 +15,10 @@ and configuration files carry over unchanged.  Differences:
   head of a token range and all of K/V streams through the ring once per
   block.  ``"head_groups"`` keeps every token of a group of K/V heads (with
   their query heads) in HBM at once, so each byte of Q, K and V crosses PCIe
-  once per run; it returns the output to host memory (``output_mode``
-  ``"host"`` or ``"host_aliased"``), and its results equal the default
-  schedule's bit for bit.
+  once per run; it writes a host or a device output but no device consumer,
+  and its results equal the default schedule's bit for bit.  ``"auto"``
+  plans head groups when they fit the budget and the output is not a device
+  consumer's, and Q blocks otherwise.
 """
 
 from __future__ import annotations
@@ -26,7 +27,7 @@ from dataclasses import dataclass, field
 
 BACKENDS = {"auto", "hip", "triton", "reference"}
 OUTPUT_MODES = {"host", "host_aliased", "device_consumer"}
-SCHEDULES = {"q_blocks", "head_groups"}
+SCHEDULES = {"q_blocks", "head_groups", "auto"}
 
 
 @dataclass(frozen=True)
@@ -67,7 +68,8 @@ class StreamingAttentionConfig:
     resident_scratch_limit_bytes: int | None = None
     # "q_blocks": the reference's Q super-block schedule.  "head_groups":
     # every token of a group of K/V heads resident at once (Q, K and V cross
-    # PCIe once; host output only).
+    # PCIe once; no device consumer).  "auto": head groups when they fit,
+    # else Q blocks.
     schedule: str = "q_blocks"
 
     def validate(self) -> None:
@@ -96,10 +98,10 @@ class StreamingAttentionConfig:
         if self.backend not in BACKENDS:
             raise ValueError(f"unsupported backend: {self.backend}")
         if self.schedule not in SCHEDULES:
-            raise ValueError("schedule must be 'q_blocks' or 'head_groups'")
+            raise ValueError("schedule must be 'q_blocks', 'head_groups' or 'auto'")
         if self.schedule == "head_groups" and self.output_mode == "device_consumer":
-            raise ValueError("schedule='head_groups' returns the output to host memory; "
-                             "device_consumer output needs schedule='q_blocks'")
+            raise ValueError("schedule='head_groups' writes a host or device output but has no "
+                             "device consumer; device_consumer output needs schedule='q_blocks'")
 
 
 @dataclass(frozen=True)

@@ -252,8 +252,9 @@ class PagedAttentionRunner:
         if kv_layout.storage_dtype == "int8" and (q_layout.head_dim % 16 or q_layout.head_dim > 128):
             raise ValueError("INT8 K/V pages need head_dim a multiple of 16 and at most 128")
         attention = config.attention
-        if attention.schedule != "q_blocks":
+        if attention.schedule == "head_groups":
             raise ValueError("paged runs gather pages into Q blocks: they need schedule='q_blocks'")
+        attention = replace(attention, schedule="q_blocks")  # "auto" plans Q blocks here
         if device_mode:
             attention = replace(attention, output_mode="device_consumer")
         plan = build_plan(

@@ -389,7 +389,9 @@ def build_plan(
     ranked by the modeled run time of this pipeline instead of the
     reference's fixed-constant cost.  With ``config.schedule ==
     "head_groups"`` the plan sizes head-group buffer sets instead (module
-    docstring)."""
+    docstring); with ``"auto"`` it does so when they fit the budget and the
+    output is not a device consumer's.  ``plan.schedule`` names the schedule
+    planned."""
     config = StreamingAttentionConfig() if config is None else config
     config.validate()
     device = torch.device(device)
@@ -435,7 +437,11 @@ def build_plan(
             cost = modeled_run(**sizes, rates=rates, **shape)[0]
         scored.append((cost, q_chunk, kv_chunk))
 
-    if config.schedule == "head_groups":
+    head_groups = config.schedule == "head_groups" or (
+        config.schedule == "auto" and config.output_mode != "device_consumer"
+        and _head_group_layout(budget=config.workspace_budget_bytes, max_q_tokens=max_q_tokens,
+                               max_kv_tokens=max_kv_tokens, **shape) is not None)
+    if head_groups:
         # The default schedule's K/V chunk for the same inputs (row sums merge
         # there), rounded to whole 64-key tiles when a segment can be longer.
         if scored:

@@ -30,6 +30,7 @@ from __future__ import annotations
 
 import time
 from contextlib import nullcontext
+from dataclasses import replace
 
 import torch
 
@@ -54,8 +55,10 @@ class ProjectedAttentionRunner:
         self.pipeline_config = ProjectionPipelineConfig() if pipeline_config is None else pipeline_config
         self.attention_config.validate()
         self.pipeline_config.validate()
-        if self.attention_config.schedule != "q_blocks":
+        if self.attention_config.schedule == "head_groups":
             raise ValueError("the projected pipeline projects each finished Q tile: it needs schedule='q_blocks'")
+        # "auto" plans Q blocks here: the output projection consumes Q tiles.
+        self.attention_config = replace(self.attention_config, schedule="q_blocks")
         # The plan is rebuilt against the runner's own attention config, as
         # the reference does, so a plan made with other launch settings
         # still gets a consistent workspace.

@@ -251,3 +251,25 @@ def test_schedule_validation():
     with pytest.raises(ValueError, match="device_consumer"):
         StreamingAttentionConfig(schedule="head_groups", output_mode="device_consumer").validate()
     StreamingAttentionConfig(schedule="head_groups", output_mode="host_aliased").validate()
+
+
+def test_auto_schedule_plans_head_groups_when_they_fit():
+    config = StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30, schedule="auto")
+    shape = dict(q_heads=56, kv_heads=56, head_dim=128, dtype=torch.bfloat16, device="cpu", max_q_tokens=524_288,
+                 max_kv_tokens=524_288)
+    plan = build_plan(config=config, **shape)
+    assert (plan.schedule, plan.head_group_kv_heads, plan.head_group_sets) == ("head_groups", 1, 2)
+    # A device consumer finishes Q tiles: Q blocks, the reference's plan.
+    consumer = StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30, schedule="auto",
+                                        output_mode="device_consumer")
+    plan = build_plan(config=consumer, **shape)
+    reference = build_plan(config=StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30,
+                                                           output_mode="device_consumer"), **shape)
+    assert plan.schedule == "q_blocks" and plan == reference
+    # 320 MiB holds no head of 524,288 tokens (403 MB without V transposed,
+    # plus the margin): Q blocks.
+    small = StreamingAttentionConfig(workspace_budget_bytes=320 * 2**20, schedule="auto")
+    plan = build_plan(config=small, **shape)
+    assert plan.schedule == "q_blocks"
+    assert plan.q_chunk_tokens == build_plan(config=StreamingAttentionConfig(workspace_budget_bytes=320 * 2**20),
+                                             **shape).q_chunk_tokens
