@@ -266,7 +266,10 @@ int32_t sa_pipeline_destroy(sa_pipeline* pipeline);
  * as the block's last chunk launches finish piece by piece, and the next
  * block's first chunk is copied ahead of its Q rows and applied to each
  * piece as its rows land; every row still sees the same chunks in the same
- * order.  Returns after the D2H stream has drained.
+ * order.  Returns after the D2H stream has drained.  An error return comes
+ * after the pipeline's copy streams and second stream have drained, so no
+ * copy still reads or writes the host buffers; launches already enqueued on
+ * compute_stream may still run.
  *
  *   q_host/k_host/v_host/out_host: contiguous pinned host [tokens, heads, head_dim] dtype
  *   cu_seqlens_q/k: num_segments + 1 host int64 boundaries
@@ -289,8 +292,10 @@ int32_t sa_pipeline_run(
  * output copy is made.  Enqueued on compute_stream (and the pipeline's
  * second stream, joined back into it); returns once the host inputs have
  * been copied, before the launches end: later work on compute_stream sees
- * the output and the LSE.  No counterpart in the reference (its device
- * outputs go through output_transform, executor.py:145-172).
+ * the output and the LSE.  An error return comes after the copy streams and
+ * the second stream have drained, as for sa_pipeline_run.  No counterpart in
+ * the reference (its device outputs go through output_transform,
+ * executor.py:145-172).
  */
 int32_t sa_pipeline_run_device_output(
     sa_pipeline* pipeline,

@@ -1212,6 +1212,83 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
   return 0;
 }
 
+// sa_pipeline_run's schedules, dispatched by the pipeline's kind and output
+// slots (the caller's device is current).
+int32_t run_host_output(sa_pipeline* p, const void* q_host, const void* k_host, const void* v_host,
+                        void* out_host, float* lse, int64_t lse_stride_h, const int64_t* cu_seqlens_q,
+                        const int64_t* cu_seqlens_k, int32_t num_segments, double softmax_scale,
+                        int32_t causal, void* compute_stream, sa_pipeline_stats* stats) {
+  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
+  const char* qh = static_cast<const char*>(q_host);
+  const char* kh = static_cast<const char*>(k_host);
+  const char* vh = static_cast<const char*>(v_host);
+  char* oh = static_cast<char*>(out_host);
+  if (p->head_groups)
+    return run_head_groups(p, qh, kh, vh, oh, lse, lse_stride_h, cu_seqlens_q, cu_seqlens_k, num_segments,
+                           softmax_scale, causal, compute, stats);
+  if (!p->has_out_slots || p->num_out == 1) {
+    std::vector<Pass> passes;
+    for (int32_t s = 0; s < num_segments; ++s) {
+      const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
+      const int64_t k_start = cu_seqlens_k[s], k_stop = cu_seqlens_k[s + 1];
+      const int64_t q_length = q_stop - q_start, k_length = k_stop - k_start;
+      if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0)) {
+        sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
+        return SA_ERR_INVALID_ARGUMENT;
+      }
+      const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
+      for (int64_t qt = q_start; qt < q_stop; qt += block)
+        passes.push_back(Pass{qt, k_start, (int32_t)std::min<int64_t>(block, q_stop - qt), (int32_t)k_length,
+                              (int32_t)(qt - q_start), (int32_t)(k_length - q_length)});
+    }
+    if (!p->has_out_slots)
+      return run_aliased(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
+    return run_alternating(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
+  }
+  int64_t chunk_index = 0;
+  for (int32_t s = 0; s < num_segments; ++s) {
+    const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
+    const int64_t k_start = cu_seqlens_k[s], k_stop = cu_seqlens_k[s + 1];
+    const int64_t q_length = q_stop - q_start, k_length = k_stop - k_start;
+    if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0)) {
+      sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
+      return SA_ERR_INVALID_ARGUMENT;
+    }
+    const int32_t causal_shift = (int32_t)(k_length - q_length);
+    const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
+    for (int64_t qt = q_start; qt < q_stop; qt += block) {
+      const int32_t n = (int32_t)std::min<int64_t>(block, q_stop - qt);
+      // Two output slots: the block is finalized into slot i % 2 and copied
+      // out while the next block streams.
+      int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
+      if (rc) return rc;
+      rc = stream_kv(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
+                     (int32_t)k_length, n, (int32_t)(qt - q_start), causal_shift, softmax_scale,
+                     causal, compute, stats);
+      if (rc) return rc;
+      const int32_t slot = (int32_t)(chunk_index % p->num_out);
+      const int64_t bytes = (int64_t)n * p->q_row_bytes;
+      rc = finalize(p, slot, n, lse, lse_stride_h, qt, compute);
+      if (rc) return rc;
+      rc = d2h(p, oh + qt * p->q_row_bytes, p->out_slots[slot], bytes, slot, 0, compute, stats);
+      if (rc) return rc;
+      ++chunk_index;
+    }
+  }
+  SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
+  return 0;
+}
+
+// After a failed run, copies enqueued before the failure may still read the
+// host inputs or write the host output, and the pipeline's second stream may
+// still run launches: wait for them, so that the caller may release its
+// buffers once the call returns.  The error reported stays the first one.
+void drain_after_error(sa_pipeline* p) {
+  if (p->h2d) (void)hipStreamSynchronize(p->h2d);
+  if (p->d2h) (void)hipStreamSynchronize(p->d2h);
+  if (p->side) (void)hipStreamSynchronize(p->side);
+}
+
 }  // namespace
 
 extern "C" {
@@ -1896,10 +1973,13 @@ int32_t sa_pipeline_run_device_output(sa_pipeline* p, const void* q_host, const 
   }
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
-  return run_head_groups(p, static_cast<const char*>(q_host), static_cast<const char*>(k_host),
-                         static_cast<const char*>(v_host), nullptr, lse, lse_stride_h, cu_seqlens_q, cu_seqlens_k,
-                         num_segments, softmax_scale, causal, static_cast<hipStream_t>(compute_stream), stats,
-                         static_cast<char*>(out), stride_ot, stride_oh);
+  const int32_t rc = run_head_groups(p, static_cast<const char*>(q_host), static_cast<const char*>(k_host),
+                                     static_cast<const char*>(v_host), nullptr, lse, lse_stride_h, cu_seqlens_q,
+                                     cu_seqlens_k, num_segments, softmax_scale, causal,
+                                     static_cast<hipStream_t>(compute_stream), stats, static_cast<char*>(out),
+                                     stride_ot, stride_oh);
+  if (rc != 0) drain_after_error(p);
+  return rc;
 }
 
 int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, const void* v_host,
@@ -1915,65 +1995,10 @@ int32_t sa_pipeline_run(sa_pipeline* p, const void* q_host, const void* k_host, 
   }
   sa::DeviceGuard guard(p->device);
   SA_HIP_RETURN(guard.status());
-  hipStream_t compute = static_cast<hipStream_t>(compute_stream);
-  const char* qh = static_cast<const char*>(q_host);
-  const char* kh = static_cast<const char*>(k_host);
-  const char* vh = static_cast<const char*>(v_host);
-  char* oh = static_cast<char*>(out_host);
-  if (p->head_groups)
-    return run_head_groups(p, qh, kh, vh, oh, lse, lse_stride_h, cu_seqlens_q, cu_seqlens_k, num_segments,
-                           softmax_scale, causal, compute, stats);
-  if (!p->has_out_slots || p->num_out == 1) {
-    std::vector<Pass> passes;
-    for (int32_t s = 0; s < num_segments; ++s) {
-      const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
-      const int64_t k_start = cu_seqlens_k[s], k_stop = cu_seqlens_k[s + 1];
-      const int64_t q_length = q_stop - q_start, k_length = k_stop - k_start;
-      if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0)) {
-        sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
-        return SA_ERR_INVALID_ARGUMENT;
-      }
-      const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
-      for (int64_t qt = q_start; qt < q_stop; qt += block)
-        passes.push_back(Pass{qt, k_start, (int32_t)std::min<int64_t>(block, q_stop - qt), (int32_t)k_length,
-                              (int32_t)(qt - q_start), (int32_t)(k_length - q_length)});
-    }
-    if (!p->has_out_slots)
-      return run_aliased(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
-    return run_alternating(p, qh, kh, vh, oh, lse, lse_stride_h, passes, softmax_scale, causal, compute, stats);
-  }
-  int64_t chunk_index = 0;
-  for (int32_t s = 0; s < num_segments; ++s) {
-    const int64_t q_start = cu_seqlens_q[s], q_stop = cu_seqlens_q[s + 1];
-    const int64_t k_start = cu_seqlens_k[s], k_stop = cu_seqlens_k[s + 1];
-    const int64_t q_length = q_stop - q_start, k_length = k_stop - k_start;
-    if (q_length < 0 || k_length < 0 || (q_length > 0 && k_length == 0)) {
-      sa::set_error("sa_pipeline_run: segment %d has invalid bounds", s);
-      return SA_ERR_INVALID_ARGUMENT;
-    }
-    const int32_t causal_shift = (int32_t)(k_length - q_length);
-    const int64_t block = pass_rows(q_length, p->q_chunk, sa::update_block_rows(p->head_dim));
-    for (int64_t qt = q_start; qt < q_stop; qt += block) {
-      const int32_t n = (int32_t)std::min<int64_t>(block, q_stop - qt);
-      // Two output slots: the block is finalized into slot i % 2 and copied
-      // out while the next block streams.
-      int32_t rc = load_q(p, qh + qt * p->q_row_bytes, n, compute, stats);
-      if (rc) return rc;
-      rc = stream_kv(p, kh + k_start * p->kv_row_bytes, vh + k_start * p->kv_row_bytes,
-                     (int32_t)k_length, n, (int32_t)(qt - q_start), causal_shift, softmax_scale,
-                     causal, compute, stats);
-      if (rc) return rc;
-      const int32_t slot = (int32_t)(chunk_index % p->num_out);
-      const int64_t bytes = (int64_t)n * p->q_row_bytes;
-      rc = finalize(p, slot, n, lse, lse_stride_h, qt, compute);
-      if (rc) return rc;
-      rc = d2h(p, oh + qt * p->q_row_bytes, p->out_slots[slot], bytes, slot, 0, compute, stats);
-      if (rc) return rc;
-      ++chunk_index;
-    }
-  }
-  SA_HIP_RETURN(hipStreamSynchronize(p->d2h));
-  return 0;
+  const int32_t rc = run_host_output(p, q_host, k_host, v_host, out_host, lse, lse_stride_h, cu_seqlens_q,
+                                     cu_seqlens_k, num_segments, softmax_scale, causal, compute_stream, stats);
+  if (rc != 0) drain_after_error(p);
+  return rc;
 }
 
 }  // extern "C"

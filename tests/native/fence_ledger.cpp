@@ -15,7 +15,10 @@
 // and every device-to-host copy must be complete at the last host
 // synchronization, where the pipeline returns the host output to its caller.
 // ledger_drop_wait(n) makes the n-th stream-wait call a no-op: a planted
-// ordering mistake the check must report.
+// ordering mistake the check must report.  ledger_fail_copy(n) makes the n-th
+// copy call fail (nothing is recorded for it): an error in the middle of a
+// run, after which ledger_unfinished() counts the copies and host functions
+// that were not complete when the call returned.
 
 #include <hip/hip_runtime.h>
 
@@ -57,9 +60,14 @@ struct Ledger {
   long waits_seen = 0;
   long drop_wait = -1;
   long dropped = 0;
+  long copies_seen = 0;
+  long fail_copy = -1;
 };
 
 Ledger g;
+
+// Whether this copy call is the one planted to fail.
+bool copy_fails() { return g.copies_seen++ == g.fail_copy; }
 
 int stream_id(hipStream_t s) {
   auto it = g.stream_ids.find(s);
@@ -185,6 +193,7 @@ hipError_t hipEventElapsedTime(float* ms, hipEvent_t, hipEvent_t) {
   return hipSuccess;
 }
 hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKind kind, hipStream_t stream) {
+  if (copy_fails()) return hipErrorInvalidValue;
   const Kind k = kind == hipMemcpyHostToDevice ? kCopyH2D : kind == hipMemcpyDeviceToHost ? kCopyD2H : kCopyD2D;
   push(Op{k, stream_id(stream), -1, {span(src, (int64_t)bytes)}, {span(dst, (int64_t)bytes)},
           k == kCopyH2D ? "h2d copy" : k == kCopyD2H ? "d2h copy" : "d2d copy"});
@@ -194,6 +203,7 @@ hipError_t hipMemcpyAsync(void* dst, const void* src, size_t bytes, hipMemcpyKin
 // A strided copy reads and writes rows of `width` bytes on each side.
 hipError_t hipMemcpy2DAsync(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width, size_t height,
                             hipMemcpyKind kind, hipStream_t stream) {
+  if (copy_fails()) return hipErrorInvalidValue;
   const Kind k = kind == hipMemcpyHostToDevice ? kCopyH2D : kind == hipMemcpyDeviceToHost ? kCopyD2H : kCopyD2D;
   push(Op{k, stream_id(stream), -1, {strided(src, (int64_t)width, (int64_t)spitch, (int64_t)height)},
           {strided(dst, (int64_t)width, (int64_t)dpitch, (int64_t)height)},
@@ -295,9 +305,15 @@ void ledger_reset(void) {
   g.waits_seen = 0;
   g.drop_wait = -1;
   g.dropped = 0;
+  g.copies_seen = 0;
+  g.fail_copy = -1;
 }
 
 void ledger_drop_wait(long n) { g.drop_wait = n; }
+
+void ledger_fail_copy(long n) { g.fail_copy = n; }
+
+long ledger_copies(void) { return g.copies_seen; }
 
 long ledger_waits(void) { return g.waits_seen; }
 
@@ -375,6 +391,42 @@ int64_t ledger_check(char* msg, int64_t msg_len) {
   }
   if (msg && msg_len > 0) snprintf(msg, (size_t)msg_len, "%s", text.c_str());
   return violations;
+}
+
+// Copies and host functions (they touch host memory) not ordered before the
+// last host synchronization recorded so far.
+int64_t ledger_unfinished(void) {
+  const int n = (int)g.ops.size();
+  int last_sync = -1;
+  for (int j = 0; j < n; ++j)
+    if (g.ops[j].kind == kStreamSync || g.ops[j].kind == kEventSync) last_sync = j;
+  // Stream order, waits and earlier synchronizations, as in ledger_check.
+  std::vector<std::vector<char>> reach(n, std::vector<char>(n, 0));
+  std::map<int, int> last_on_stream;
+  int barrier = -1;
+  for (int j = 0; j < n; ++j) {
+    const Op& op = g.ops[j];
+    std::vector<int> preds;
+    if (op.stream >= 0) {
+      auto it = last_on_stream.find(op.stream);
+      if (it != last_on_stream.end()) preds.push_back(it->second);
+    }
+    if ((op.kind == kWait || op.kind == kEventSync) && op.source >= 0) preds.push_back(op.source);
+    if (barrier >= 0) preds.push_back(barrier);
+    for (int p : preds) {
+      for (int i = 0; i < n; ++i) reach[j][i] |= reach[p][i];
+      reach[j][p] = 1;
+    }
+    if (op.stream >= 0) last_on_stream[op.stream] = j;
+    if (op.kind == kStreamSync || op.kind == kEventSync) barrier = j;
+  }
+  int64_t unfinished = 0;
+  for (int i = 0; i < n; ++i) {
+    const Kind k = g.ops[i].kind;
+    const bool host_side = k == kCopyH2D || k == kCopyD2H || (k == kKernel && g.ops[i].label == "host function");
+    if (host_side && (last_sync < i || !reach[last_sync][i])) ++unfinished;
+  }
+  return unfinished;
 }
 
 }  // extern "C"

@@ -53,6 +53,9 @@ def ledger(tmp_path_factory):
     lib.ledger_waits.restype = ctypes.c_long
     lib.ledger_dropped.restype = ctypes.c_long
     lib.ledger_counts.argtypes = [ctypes.POINTER(ctypes.c_int64)]
+    lib.ledger_fail_copy.argtypes = [ctypes.c_long]
+    lib.ledger_copies.restype = ctypes.c_long
+    lib.ledger_unfinished.restype = ctypes.c_int64
     return lib
 
 
@@ -500,3 +503,78 @@ def test_head_group_schedule_into_device_output_is_race_free(ledger, num_sets):
     ledger.ledger_counts(counts)
     assert list(counts) == [0, 0, 0, 0]
     assert ledger.sa_pipeline_destroy(handle) == 0
+
+
+def _failing_runs(ledger, run, label):
+    """Make each copy of a run fail in turn: the call reports the error, and
+    no copy it enqueued (nor a host function) is still running when it
+    returns, so the caller may release its buffers."""
+    ledger.ledger_reset()
+    status, unfinished = run()
+    assert status == 0 and unfinished == 0, label
+    copies = ledger.ledger_copies()
+    assert copies > 3
+    for n in range(copies):
+        ledger.ledger_reset()
+        ledger.ledger_fail_copy(n)
+        status, unfinished = run()
+        assert status != 0, f"{label}: copy {n} failed, the run reported success"
+        assert unfinished == 0, f"{label}: copy {n} failed, {unfinished} copies in flight at the return"
+
+
+@pytest.mark.parametrize("num_out,out_slots", [(1, True), (2, True), (0, False)])
+def test_a_failed_tensor_mode_run_returns_with_its_copies_drained(ledger, num_out, out_slots):
+    host = Space(0x5000_0000_0000)
+    q_lengths, k_lengths = [3000, 700], [2600, 900]
+    cu_q, q_b = bounds(q_lengths)
+    cu_k, k_b = bounds(k_lengths)
+
+    def run():
+        p = Pipeline(ledger, q_chunk=1024, kv_chunk=256, q_heads=4, kv_heads=2, head_dim=64, num_kv=2,
+                     num_out=max(num_out, 1), out_slots=out_slots)
+        q_host, k_host = host.take(q_b[-1] * p.q_row), host.take(k_b[-1] * p.kv_row)
+        v_host, out_host = host.take(k_b[-1] * p.kv_row), host.take(q_b[-1] * p.q_row)
+        status = ledger.sa_pipeline_run(p.handle, q_host, k_host, v_host, out_host, None, 0, cu_q, cu_k, 2, 0.125, 0,
+                                        p.compute, None)
+        unfinished = ledger.ledger_unfinished()
+        p.destroy()
+        return status, unfinished
+
+    _failing_runs(ledger, run, f"tensor mode, {num_out} output slots")
+
+
+@pytest.mark.parametrize("num_sets", [1, 2])
+@pytest.mark.parametrize("device_output", [False, True])
+def test_a_failed_head_group_run_returns_with_its_copies_drained(ledger, num_sets, device_output):
+    q_heads, kv_heads, head_dim = 4, 4, 64
+    q_lengths, k_lengths = [1500, 900], [1200, 900]
+    dev = Space(0x7000_0000_0000)
+    host = Space(0x5000_0000_0000)
+    cu_q, q_b = bounds(q_lengths)
+    cu_k, k_b = bounds(k_lengths)
+    tq, tk = q_b[-1], k_b[-1]
+    row = q_heads * head_dim * HEAD_BYTES
+
+    def run():
+        qo = [dev.take(tq * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+        ks = [dev.take(tk * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+        vs = [dev.take(tk * head_dim * HEAD_BYTES) for _ in range(num_sets)]
+        handle = ctypes.c_void_p()
+        assert ledger.sa_pipeline_create_head_groups(
+            ctypes.byref(handle), 0, (ctypes.c_void_p * 2)(*qo), (ctypes.c_void_p * 2)(*ks),
+            (ctypes.c_void_p * 2)(*vs), None, 0, num_sets, tq, tk, 1, 256, q_heads, kv_heads, head_dim, 0, None,
+            None) == 0
+        q_host, k_host, v_host = host.take(tq * row), host.take(tk * row), host.take(tk * row)
+        if device_output:
+            status = ledger.sa_pipeline_run_device_output(handle, q_host, k_host, v_host, dev.take(tq * row),
+                                                          q_heads * head_dim, head_dim, None, 0, cu_q, cu_k, 2,
+                                                          0.125, 0, 0xC0FFEE, None)
+        else:
+            status = ledger.sa_pipeline_run(handle, q_host, k_host, v_host, host.take(tq * row), None, 0, cu_q,
+                                            cu_k, 2, 0.125, 0, 0xC0FFEE, None)
+        unfinished = ledger.ledger_unfinished()
+        assert ledger.sa_pipeline_destroy(handle) == 0
+        return status, unfinished
+
+    _failing_runs(ledger, run, f"head groups, sets={num_sets}, device output={device_output}")
+
