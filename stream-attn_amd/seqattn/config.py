@@ -17,8 +17,8 @@ and configuration files carry over unchanged.  Differences:
   their query heads) in HBM at once, so each byte of Q, K and V crosses PCIe
   once per run; it writes a host or a device output but no device consumer,
   and its results equal the default schedule's bit for bit.  ``"auto"``
-  plans head groups when they fit the budget and the output is not a device
-  consumer's, and Q blocks otherwise.
+  plans head groups when they fit the budget, the output is not a device
+  consumer's and ``require_pinned`` holds, and Q blocks otherwise.
 """
 
 from __future__ import annotations
@@ -68,8 +68,8 @@ class StreamingAttentionConfig:
     resident_scratch_limit_bytes: int | None = None
     # "q_blocks": the reference's Q super-block schedule.  "head_groups":
     # every token of a group of K/V heads resident at once (Q, K and V cross
-    # PCIe once; no device consumer).  "auto": head groups when they fit,
-    # else Q blocks.
+    # PCIe once; no device consumer).  "auto": head groups when they fit
+    # (with require_pinned and no device consumer), else Q blocks.
     schedule: str = "q_blocks"
 
     def validate(self) -> None:

@@ -389,8 +389,9 @@ def build_plan(
     ranked by the modeled run time of this pipeline instead of the
     reference's fixed-constant cost.  With ``config.schedule ==
     "head_groups"`` the plan sizes head-group buffer sets instead (module
-    docstring); with ``"auto"`` it does so when they fit the budget and the
-    output is not a device consumer's.  ``plan.schedule`` names the schedule
+    docstring); with ``"auto"`` it does so when they fit the budget, the
+    output is not a device consumer's and the inputs must be page-locked
+    (``require_pinned``).  ``plan.schedule`` names the schedule
     planned."""
     config = StreamingAttentionConfig() if config is None else config
     config.validate()
@@ -437,8 +438,10 @@ def build_plan(
             cost = modeled_run(**sizes, rates=rates, **shape)[0]
         scored.append((cost, q_chunk, kv_chunk))
 
+    # "auto" takes head groups only where the runner can run them: a host
+    # output and page-locked inputs (the head columns move by strided copies).
     head_groups = config.schedule == "head_groups" or (
-        config.schedule == "auto" and config.output_mode != "device_consumer"
+        config.schedule == "auto" and config.output_mode != "device_consumer" and config.require_pinned
         and _head_group_layout(budget=config.workspace_budget_bytes, max_q_tokens=max_q_tokens,
                                max_kv_tokens=max_kv_tokens, **shape) is not None)
     if head_groups:

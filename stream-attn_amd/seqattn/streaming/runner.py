@@ -213,8 +213,9 @@ class StreamingAttentionRunner(HipExecutorMixin):
         if q_cpu.device.type != "cpu":
             raise ValueError("seqattn expects CPU-backed q, k, and v tensors")
         if self.plan.schedule == "head_groups":
-            raise ValueError("run_with_device_output needs schedule='q_blocks' (head groups finish every "
-                             "query row of a head group at once, not tile by tile)")
+            raise ValueError("run_with_device_output needs a Q-block plan (schedule='q_blocks', or "
+                             "output_mode='device_consumer' with schedule='auto'): head groups finish every "
+                             "query row of a head group at once, not tile by tile")
         q_bounds, k_bounds = self._validate_inputs(q_cpu, k_cpu, v_cpu, cu_seqlens_q, cu_seqlens_k)
         if out.device.type not in {"cpu", "cuda"} or out.shape[0] != q_cpu.shape[0]:
             raise ValueError("out must be a CPU tensor with one row per query token")

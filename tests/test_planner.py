@@ -273,3 +273,7 @@ def test_auto_schedule_plans_head_groups_when_they_fit():
     assert plan.schedule == "q_blocks"
     assert plan.q_chunk_tokens == build_plan(config=StreamingAttentionConfig(workspace_budget_bytes=320 * 2**20),
                                              **shape).q_chunk_tokens
+    # Pageable inputs allowed (require_pinned=False): head columns cannot
+    # move by strided copies from them, so Q blocks.
+    pageable = StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30, schedule="auto", require_pinned=False)
+    assert build_plan(config=pageable, **shape).schedule == "q_blocks"
