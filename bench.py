@@ -28,10 +28,13 @@ strided copies land.  Beside it, from the same run:
   step over all queries and keys with the finalize fused (no PCIe);
 * host_aliased: the Q-block step with each pass's output finalized into its
   Q block (no output slot in the budget, 14 passes instead of 19);
-* cpu_baseline: the CPU oracle (numpy restatement of the reference's chunked
-  FP32 attention) timed on this host on a bounded row sample, which is also
-  the parity check of the sampled rows (O and LSE) of every leg, and the
-  legs' bit-identity on those rows;
+* parity: the CPU oracle (numpy restatement of the reference's chunked FP32
+  attention) on a bounded row sample, against the sampled rows (O and LSE)
+  of every leg, and the legs' bit-identity on those rows;
+* cpu_baseline: the reference's CPU chunked attention restated with
+  torch.matmul in float32, timed on this host's cores (torch's intra-op
+  threads) on the same rows, with its agreement with the oracle and the
+  oracle's own rate beside it;
 * config2_65k, config4_paged and config5_1m: the benchmark's other
   configurations, measured after the headline legs' buffers are released
   (65,536 tokens x 32 heads resident and streamed with 1 GiB; 158,208
@@ -616,21 +619,20 @@ def main() -> int:
                          "rows: 0, N/4, N/2, 3N/4, N-1 and seeded-random rows, all heads",
         }
         sample_flop = 4 * h * d * rows.size * n
-        cpu_tflops = sample_flop / cpu_s / 1e12
+        log(f"CPU baseline: torch restatement on {rows.size} rows, {threads} threads")
+        torch_s, agree = torch_cpu_sample(q[torch.from_numpy(rows)], k, v, plan.kv_chunk_tokens, threads,
+                                          ref_o, ref_l)
+        cpu_tflops = sample_flop / torch_s / 1e12
         hosts = cpu_share()[1]
-        cpu_baseline = {
-            "value": cpu_tflops,
-            "unit": "TFLOPS",
-            "cores": threads,
-            "kind": "port",
-            "host_cpus": hosts,
-            "sample": f"{rows.size} query rows x {h} heads x all {n} keys (kv chunk {plan.kv_chunk_tokens}); "
-                      f"{cpu_s:.1f} s, extrapolated full step {flop / (cpu_tflops * 1e12):.0f} s; "
-                      f"numpy float32, heads split over {threads} threads (single-threaded BLAS each): this "
-                      f"process's CPU share on a host with {hosts['host_logical_cpus']} logical CPUs",
-        }
+        cpu_baseline = cpu_baseline_entry(
+            sample_flop, torch_s, threads,
+            f"{rows.size} query rows x {h} heads x all {n} keys (kv chunk {plan.kv_chunk_tokens}), "
+            f"extrapolated full step {flop / (cpu_tflops * 1e12):.0f} s, this process's CPU share on a host "
+            f"with {hosts['host_logical_cpus']} logical CPUs", agree, cpu_s)
+        cpu_baseline["host_cpus"] = hosts
         log(f"parity max|dO| = {err_o:.3e} max|dLSE| = {err_l:.3e} {errors} relL2 {rel_l2}; "
-            f"CPU oracle {cpu_tflops:.4f} TFLOPS on {threads} threads")
+            f"CPU baseline {cpu_tflops:.4f} TFLOPS on {threads} threads (numpy oracle "
+            f"{sample_flop / cpu_s / 1e12:.4f}); torch vs oracle {agree}")
 
     kernel_tflops = head["kernel_tflops"]
     traffic_file = args.traffic_file
@@ -817,11 +819,57 @@ def oracle_sample(q, k, v, rows, kv_chunk, workers, scale=None):
     return ref_o, ref_l, time.perf_counter() - t0
 
 
+def torch_cpu_sample(q_rows, k, v, kv_chunk, threads, ref_o=None, ref_l=None, scale=None):
+    """The CPU baseline: the reference's CPU chunked attention restated with
+    torch.matmul in float32 (oracle/seqattn_torch_cpu.py), timed on torch's
+    intra-op threads over query rows ``q_rows`` (bf16 tensors) against all
+    keys of one segment.  Returns (seconds, agreement with the numpy oracle's
+    ``ref_o``/``ref_l`` or None)."""
+    import numpy as np
+    import torch
+
+    from oracle.seqattn_torch_cpu import chunked_attention_torch
+
+    n = k.shape[0]
+    previous = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    try:
+        t0 = time.perf_counter()
+        got_o, got_l = chunked_attention_torch(q_rows, k, v, [0, q_rows.shape[0]], [0, n],
+                                               q_chunk_tokens=q_rows.shape[0], kv_chunk_tokens=kv_chunk,
+                                               softmax_scale=scale, head_batch=8)
+        seconds = time.perf_counter() - t0
+    finally:
+        torch.set_num_threads(previous)
+    agree = None
+    if ref_o is not None:
+        agree = {"max_abs_o": float(np.abs(got_o.numpy() - ref_o).max()),
+                 "max_abs_lse": float(np.abs(got_l.numpy() - ref_l).max()) if ref_l is not None else None}
+    return seconds, agree
+
+
+def cpu_baseline_entry(flop, seconds, threads, sample, agree=None, oracle_seconds=None) -> dict:
+    """The ``cpu_baseline`` object of a result line (the torch restatement's
+    timing; the numpy oracle's beside it)."""
+    entry = {"value": flop / seconds / 1e12, "unit": "TFLOPS", "cores": threads, "kind": "port",
+             "sample": f"{sample}; {seconds:.2f} s; the reference's CPU chunked attention restated with "
+                       f"torch.matmul in float32 (oracle/seqattn_torch_cpu.py) on {threads} intra-op threads"}
+    if oracle_seconds is not None:
+        entry["numpy_oracle_tflops"] = flop / oracle_seconds / 1e12
+    if agree is not None:
+        entry["vs_numpy_oracle"] = agree
+    return entry
+
+
 def sampled_parity(q, k, v, out, lse, rows, kv_chunk, workers, scale=None):
-    """Oracle O (and LSE) on sampled query rows against the GPU result; also
-    the CPU baseline timing (returns parity dict, seconds)."""
-    ref_o, ref_l, cpu_s = oracle_sample(q, k, v, rows, kv_chunk, workers, scale)
-    return compare_sample(out, lse, rows, ref_o, ref_l), cpu_s
+    """Oracle O (and LSE) on sampled query rows against the GPU result, and
+    the CPU baseline timing on the same rows: (parity dict, torch seconds,
+    agreement of the torch restatement with the oracle, oracle seconds)."""
+    import torch
+
+    ref_o, ref_l, oracle_s = oracle_sample(q, k, v, rows, kv_chunk, workers, scale)
+    torch_s, agree = torch_cpu_sample(q[torch.from_numpy(rows)], k, v, kv_chunk, workers, ref_o, ref_l, scale)
+    return compare_sample(out, lse, rows, ref_o, ref_l), torch_s, agree, oracle_s
 
 
 def compare_sample(out, lse, rows, ref_o, ref_l) -> dict:
@@ -996,10 +1044,9 @@ def measure_1m(args, steps, warmup, h2d_peak=None) -> dict:
         rng = np.random.default_rng(args.seed)
         rows = np.unique(np.concatenate([[0, n // 4, n // 2, 3 * n // 4, n - 1],
                                          rng.choice(n, args.parity_rows // 4, replace=False)]))
-        parity, cpu_s = sampled_parity(q, k, v, out, lse, rows, 8192, args.cpu_workers)
-        cpu_baseline = {"value": 4 * h * d * rows.size * n / cpu_s / 1e12, "unit": "TFLOPS",
-                        "cores": args.cpu_workers, "kind": "port",
-                        "sample": f"{rows.size} query rows x {h} heads x all {n} keys; {cpu_s:.1f} s"}
+        parity, cpu_s, agree, oracle_s = sampled_parity(q, k, v, out, lse, rows, 8192, args.cpu_workers)
+        cpu_baseline = cpu_baseline_entry(4 * h * d * rows.size * n, cpu_s, args.cpu_workers,
+                                          f"{rows.size} query rows x {h} heads x all {n} keys", agree, oracle_s)
         log(f"1m parity: {parity}")
     result = {
         "metric": "effective TFLOPS, 1M-tok BF16 MHA from pinned DRAM, 8 GiB HBM",
@@ -1068,12 +1115,11 @@ def measure_65k(args, steps, warmup, h2d_peak=None) -> dict:
         rng = np.random.default_rng(args.seed)
         rows = np.unique(np.concatenate([[0, n // 4, n // 2, 3 * n // 4, n - 1],
                                          rng.choice(n, args.parity_rows // 4, replace=False)]))
-        parity, cpu_s = sampled_parity(q, k, v, out_r, lse_r, rows, 4096, args.cpu_workers)
+        parity, cpu_s, agree, oracle_s = sampled_parity(q, k, v, out_r, lse_r, rows, 4096, args.cpu_workers)
         parity["streamed_and_resident_bit_identical"] = identical
         parity["ok"] = parity["ok"] and identical
-        cpu_baseline = {"value": 4 * h * d * rows.size * n / cpu_s / 1e12, "unit": "TFLOPS",
-                        "cores": args.cpu_workers, "kind": "port",
-                        "sample": f"{rows.size} query rows x {h} heads x all {n} keys; {cpu_s:.2f} s"}
+        cpu_baseline = cpu_baseline_entry(4 * h * d * rows.size * n, cpu_s, args.cpu_workers,
+                                          f"{rows.size} query rows x {h} heads x all {n} keys", agree, oracle_s)
     h2d_gbps = stats.h2d_bytes / steps / sec_s / 1e9
     result = {
         "metric": "effective TFLOPS, 65K-tok BF16 MHA, resident in HBM and streamed with 1 GiB",
@@ -1356,10 +1402,11 @@ def measure_paged(args, steps, warmup, h2d_peak=None) -> dict:
             parity["ok"] = bool(parity["ok"] and parity["vs_unquantized_rel_l2"] < 0.03
                                 and parity["vs_unquantized_cosine"] > 0.995)
         sample_flop = 4 * h * d * rows.size * n
-        cpu_baseline = {"value": sample_flop / cpu_s / 1e12, "unit": "TFLOPS", "cores": args.cpu_workers,
-                        "kind": "port",
-                        "sample": f"{rows.size} query rows x {h} heads x all {n} keys; {cpu_s:.1f} s; numpy "
-                                  f"float32, heads split over {args.cpu_workers} threads"}
+        as_bf16 = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)  # noqa: E731
+        torch_s, agree = torch_cpu_sample(q[torch.from_numpy(rows)], as_bf16(k_ref), as_bf16(v_ref), 8192,
+                                          args.cpu_workers, ref_o, ref_l)
+        cpu_baseline = cpu_baseline_entry(sample_flop, torch_s, args.cpu_workers,
+                                          f"{rows.size} query rows x {h} heads x all {n} keys", agree, cpu_s)
         log(f"paged parity: {parity}")
     h2d_gbps = stats.h2d_bytes / steps / sec / 1e9
     result = {

@@ -260,3 +260,41 @@ def test_head_split_and_bf16_bit_pattern_paths_equal_the_single_threaded_float_p
                                            causal=causal)
     np.testing.assert_allclose(got_o, dense_o, atol=2e-5, rtol=2e-5)
     np.testing.assert_allclose(got_l, dense_l, atol=2e-5, rtol=2e-5)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("head_batch", [None, 3])
+def test_torch_cpu_restatement_matches_the_oracle(causal, head_batch):
+    # The CPU baseline times oracle/seqattn_torch_cpu.py; it must compute what
+    # the numpy oracle computes (to float32 rounding): GQA with 8 query heads
+    # over 2 K/V heads, an empty query segment, ragged chunks, more queries
+    # than keys in the last segment (fully masked causal rows), bf16 inputs.
+    from oracle.seqattn_torch_cpu import chunked_attention_torch
+
+    gen = torch.Generator().manual_seed(11)
+    q = torch.randn(330, 8, 64, generator=gen).to(torch.bfloat16)
+    k = torch.randn(300, 2, 64, generator=gen).to(torch.bfloat16)
+    v = torch.randn(300, 2, 64, generator=gen).to(torch.bfloat16)
+    cu_q, cu_k = bounds([120, 0, 210]), bounds([200, 20, 80])
+    ref_o, ref_l = chunked_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), cu_q, cu_k,
+                                     q_chunk_tokens=64, kv_chunk_tokens=48, causal=causal)
+    got_o, got_l = chunked_attention_torch(q, k, v, cu_q, cu_k, q_chunk_tokens=64, kv_chunk_tokens=48,
+                                           causal=causal, head_batch=head_batch)
+    np.testing.assert_allclose(got_o.numpy(), ref_o, atol=2e-6, rtol=1e-5)
+    ref_inf = np.isneginf(ref_l)
+    assert np.array_equal(np.isneginf(got_l.numpy()), ref_inf)
+    assert ref_inf.any() == causal
+    np.testing.assert_allclose(got_l.numpy()[~ref_inf], ref_l[~ref_inf], atol=2e-6, rtol=1e-6)
+
+
+def test_torch_cpu_restatement_pin_catches_a_planted_mistake(monkeypatch):
+    # A scale dropped from the logits (a plausible slip) must fail the pin.
+    import oracle.seqattn_torch_cpu as torch_cpu
+
+    gen = torch.Generator().manual_seed(12)
+    q, k, v = (torch.randn(96, 2, 32, generator=gen) for _ in range(3))
+    ref_o, _ = chunked_attention(q.numpy(), k.numpy(), v.numpy(), [0, 96], [0, 96], q_chunk_tokens=32,
+                                 kv_chunk_tokens=40)
+    got_o, _ = torch_cpu.chunked_attention_torch(q, k, v, [0, 96], [0, 96], q_chunk_tokens=32,
+                                                 kv_chunk_tokens=40, softmax_scale=1.0)
+    assert np.abs(got_o.numpy() - ref_o).max() > 1e-2
