@@ -620,15 +620,15 @@ def main() -> int:
         }
         sample_flop = 4 * h * d * rows.size * n
         log(f"CPU baseline: torch restatement on {rows.size} rows, {threads} threads")
-        torch_s, agree = torch_cpu_sample(q[torch.from_numpy(rows)], k, v, plan.kv_chunk_tokens, threads,
-                                          ref_o, ref_l)
-        cpu_tflops = sample_flop / torch_s / 1e12
+        torch_s, timed, agree = torch_cpu_sample(q[torch.from_numpy(rows)], k, v, plan.kv_chunk_tokens, threads,
+                                                 ref_o, ref_l)
+        cpu_tflops = 4 * h * d * n * timed / torch_s / 1e12
         hosts = cpu_share()[1]
         cpu_baseline = cpu_baseline_entry(
-            sample_flop, torch_s, threads,
-            f"{rows.size} query rows x {h} heads x all {n} keys (kv chunk {plan.kv_chunk_tokens}), "
-            f"extrapolated full step {flop / (cpu_tflops * 1e12):.0f} s, this process's CPU share on a host "
-            f"with {hosts['host_logical_cpus']} logical CPUs", agree, cpu_s)
+            4 * h * d * n, timed, torch_s, threads,
+            f"{h} heads x all {n} keys (kv chunk {plan.kv_chunk_tokens}), extrapolated full step "
+            f"{flop / (cpu_tflops * 1e12):.0f} s, this process's CPU share on a host with "
+            f"{hosts['host_logical_cpus']} logical CPUs", agree, rows.size, cpu_s)
         cpu_baseline["host_cpus"] = hosts
         log(f"parity max|dO| = {err_o:.3e} max|dLSE| = {err_l:.3e} {errors} relL2 {rel_l2}; "
             f"CPU baseline {cpu_tflops:.4f} TFLOPS on {threads} threads (numpy oracle "
@@ -819,18 +819,27 @@ def oracle_sample(q, k, v, rows, kv_chunk, workers, scale=None):
     return ref_o, ref_l, time.perf_counter() - t0
 
 
+# FLOP of the timed CPU-baseline sample: about 10 s on a 16-core host (the
+# torch restatement runs near 0.4 TFLOPS there).
+CPU_SAMPLE_FLOP = 4e12
+
+
 def torch_cpu_sample(q_rows, k, v, kv_chunk, threads, ref_o=None, ref_l=None, scale=None):
     """The CPU baseline: the reference's CPU chunked attention restated with
     torch.matmul in float32 (oracle/seqattn_torch_cpu.py), timed on torch's
-    intra-op threads over query rows ``q_rows`` (bf16 tensors) against all
-    keys of one segment.  Returns (seconds, agreement with the numpy oracle's
-    ``ref_o``/``ref_l`` or None)."""
+    intra-op threads over the first rows of ``q_rows`` (bf16 tensors, at
+    most CPU_SAMPLE_FLOP of work) against all keys of one segment.  Returns
+    (seconds, rows timed, agreement with the numpy oracle's ``ref_o`` /
+    ``ref_l`` on those rows or None)."""
     import numpy as np
     import torch
 
     from oracle.seqattn_torch_cpu import chunked_attention_torch
 
     n = k.shape[0]
+    per_row = 4 * q_rows.shape[1] * q_rows.shape[2] * n
+    count = max(1, min(q_rows.shape[0], int(CPU_SAMPLE_FLOP // per_row)))
+    q_rows = q_rows[:count]
     previous = torch.get_num_threads()
     torch.set_num_threads(threads)
     try:
@@ -843,19 +852,23 @@ def torch_cpu_sample(q_rows, k, v, kv_chunk, threads, ref_o=None, ref_l=None, sc
         torch.set_num_threads(previous)
     agree = None
     if ref_o is not None:
-        agree = {"max_abs_o": float(np.abs(got_o.numpy() - ref_o).max()),
-                 "max_abs_lse": float(np.abs(got_l.numpy() - ref_l).max()) if ref_l is not None else None}
-    return seconds, agree
+        agree = {"max_abs_o": float(np.abs(got_o.numpy() - ref_o[:count]).max()),
+                 "max_abs_lse": float(np.abs(got_l.numpy() - ref_l[:, :count]).max()) if ref_l is not None
+                 else None}
+    return seconds, count, agree
 
 
-def cpu_baseline_entry(flop, seconds, threads, sample, agree=None, oracle_seconds=None) -> dict:
-    """The ``cpu_baseline`` object of a result line (the torch restatement's
-    timing; the numpy oracle's beside it)."""
-    entry = {"value": flop / seconds / 1e12, "unit": "TFLOPS", "cores": threads, "kind": "port",
-             "sample": f"{sample}; {seconds:.2f} s; the reference's CPU chunked attention restated with "
-                       f"torch.matmul in float32 (oracle/seqattn_torch_cpu.py) on {threads} intra-op threads"}
+def cpu_baseline_entry(row_flop, rows, seconds, threads, sample, agree=None, oracle_rows=None,
+                       oracle_seconds=None) -> dict:
+    """The ``cpu_baseline`` object of a result line: the torch restatement's
+    rate over ``rows`` query rows of ``row_flop`` each, and the numpy
+    oracle's rate over its ``oracle_rows`` beside it."""
+    entry = {"value": row_flop * rows / seconds / 1e12, "unit": "TFLOPS", "cores": threads, "kind": "port",
+             "sample": f"{rows} query rows x {sample}; {seconds:.2f} s; the reference's CPU chunked attention "
+                       f"restated with torch.matmul in float32 (oracle/seqattn_torch_cpu.py) on {threads} "
+                       f"intra-op threads"}
     if oracle_seconds is not None:
-        entry["numpy_oracle_tflops"] = flop / oracle_seconds / 1e12
+        entry["numpy_oracle_tflops"] = row_flop * oracle_rows / oracle_seconds / 1e12
     if agree is not None:
         entry["vs_numpy_oracle"] = agree
     return entry
@@ -863,13 +876,14 @@ def cpu_baseline_entry(flop, seconds, threads, sample, agree=None, oracle_second
 
 def sampled_parity(q, k, v, out, lse, rows, kv_chunk, workers, scale=None):
     """Oracle O (and LSE) on sampled query rows against the GPU result, and
-    the CPU baseline timing on the same rows: (parity dict, torch seconds,
-    agreement of the torch restatement with the oracle, oracle seconds)."""
+    the CPU baseline timing on the first of those rows: (parity dict,
+    (torch seconds, rows timed, agreement with the oracle, oracle seconds)))."""
     import torch
 
     ref_o, ref_l, oracle_s = oracle_sample(q, k, v, rows, kv_chunk, workers, scale)
-    torch_s, agree = torch_cpu_sample(q[torch.from_numpy(rows)], k, v, kv_chunk, workers, ref_o, ref_l, scale)
-    return compare_sample(out, lse, rows, ref_o, ref_l), torch_s, agree, oracle_s
+    torch_s, count, agree = torch_cpu_sample(q[torch.from_numpy(rows)], k, v, kv_chunk, workers, ref_o, ref_l,
+                                             scale)
+    return compare_sample(out, lse, rows, ref_o, ref_l), (torch_s, count, agree, oracle_s)
 
 
 def compare_sample(out, lse, rows, ref_o, ref_l) -> dict:
@@ -1044,9 +1058,9 @@ def measure_1m(args, steps, warmup, h2d_peak=None) -> dict:
         rng = np.random.default_rng(args.seed)
         rows = np.unique(np.concatenate([[0, n // 4, n // 2, 3 * n // 4, n - 1],
                                          rng.choice(n, args.parity_rows // 4, replace=False)]))
-        parity, cpu_s, agree, oracle_s = sampled_parity(q, k, v, out, lse, rows, 8192, args.cpu_workers)
-        cpu_baseline = cpu_baseline_entry(4 * h * d * rows.size * n, cpu_s, args.cpu_workers,
-                                          f"{rows.size} query rows x {h} heads x all {n} keys", agree, oracle_s)
+        parity, (cpu_s, timed, agree, oracle_s) = sampled_parity(q, k, v, out, lse, rows, 8192, args.cpu_workers)
+        cpu_baseline = cpu_baseline_entry(4 * h * d * n, timed, cpu_s, args.cpu_workers,
+                                          f"{h} heads x all {n} keys", agree, rows.size, oracle_s)
         log(f"1m parity: {parity}")
     result = {
         "metric": "effective TFLOPS, 1M-tok BF16 MHA from pinned DRAM, 8 GiB HBM",
@@ -1115,11 +1129,12 @@ def measure_65k(args, steps, warmup, h2d_peak=None) -> dict:
         rng = np.random.default_rng(args.seed)
         rows = np.unique(np.concatenate([[0, n // 4, n // 2, 3 * n // 4, n - 1],
                                          rng.choice(n, args.parity_rows // 4, replace=False)]))
-        parity, cpu_s, agree, oracle_s = sampled_parity(q, k, v, out_r, lse_r, rows, 4096, args.cpu_workers)
+        parity, (cpu_s, timed, agree, oracle_s) = sampled_parity(q, k, v, out_r, lse_r, rows, 4096,
+                                                                 args.cpu_workers)
         parity["streamed_and_resident_bit_identical"] = identical
         parity["ok"] = parity["ok"] and identical
-        cpu_baseline = cpu_baseline_entry(4 * h * d * rows.size * n, cpu_s, args.cpu_workers,
-                                          f"{rows.size} query rows x {h} heads x all {n} keys", agree, oracle_s)
+        cpu_baseline = cpu_baseline_entry(4 * h * d * n, timed, cpu_s, args.cpu_workers,
+                                          f"{h} heads x all {n} keys", agree, rows.size, oracle_s)
     h2d_gbps = stats.h2d_bytes / steps / sec_s / 1e9
     result = {
         "metric": "effective TFLOPS, 65K-tok BF16 MHA, resident in HBM and streamed with 1 GiB",
@@ -1401,12 +1416,11 @@ def measure_paged(args, steps, warmup, h2d_peak=None) -> dict:
                 np.dot(flat_got, flat_ref) / (np.linalg.norm(flat_got) * np.linalg.norm(flat_ref)))
             parity["ok"] = bool(parity["ok"] and parity["vs_unquantized_rel_l2"] < 0.03
                                 and parity["vs_unquantized_cosine"] > 0.995)
-        sample_flop = 4 * h * d * rows.size * n
         as_bf16 = lambda a: torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)  # noqa: E731
-        torch_s, agree = torch_cpu_sample(q[torch.from_numpy(rows)], as_bf16(k_ref), as_bf16(v_ref), 8192,
-                                          args.cpu_workers, ref_o, ref_l)
-        cpu_baseline = cpu_baseline_entry(sample_flop, torch_s, args.cpu_workers,
-                                          f"{rows.size} query rows x {h} heads x all {n} keys", agree, cpu_s)
+        torch_s, timed, agree = torch_cpu_sample(q[torch.from_numpy(rows)], as_bf16(k_ref), as_bf16(v_ref),
+                                                 8192, args.cpu_workers, ref_o, ref_l)
+        cpu_baseline = cpu_baseline_entry(4 * h * d * n, timed, torch_s, args.cpu_workers,
+                                          f"{h} heads x all {n} keys", agree, rows.size, cpu_s)
         log(f"paged parity: {parity}")
     h2d_gbps = stats.h2d_bytes / steps / sec / 1e9
     result = {

@@ -82,15 +82,28 @@ def _exact_result(n=300, h=3, d=16, seed=5):
 def test_sampled_parity_accepts_the_exact_result_and_times_the_cpu_baseline():
     q, k, v, out, lse = _exact_result()
     rows = np.array([0, 75, 150, 225, 299, 17, 40])
-    parity, seconds, agree, oracle_seconds = bench.sampled_parity(q, k, v, out, lse, rows, kv_chunk=64, workers=2)
+    parity, (seconds, timed, agree, oracle_seconds) = bench.sampled_parity(q, k, v, out, lse, rows, kv_chunk=64,
+                                                                           workers=2)
     assert parity["ok"] and parity["rows"] == rows.size
     assert parity["max_abs_o"] < 1e-2 and parity["max_abs_lse"] < 1e-4
-    assert seconds > 0 and oracle_seconds > 0
+    assert seconds > 0 and oracle_seconds > 0 and timed == rows.size
     # The timed torch restatement computes what the oracle computes.
     assert agree["max_abs_o"] < 1e-5 and agree["max_abs_lse"] < 1e-5
-    entry = bench.cpu_baseline_entry(4 * 4 * 64 * rows.size * 300, seconds, 2, "sample", agree, oracle_seconds)
+    entry = bench.cpu_baseline_entry(4 * 3 * 16 * 300, timed, seconds, 2, "sample", agree, rows.size, oracle_seconds)
     assert entry["kind"] == "port" and entry["cores"] == 2 and entry["value"] > 0
     assert entry["vs_numpy_oracle"] == agree and entry["numpy_oracle_tflops"] > 0
+
+
+def test_cpu_baseline_sample_is_bounded(monkeypatch):
+    # The timed rows are cut to CPU_SAMPLE_FLOP of work; the agreement is
+    # taken on those rows.
+    q, k, v, out, lse = _exact_result()
+    rows = np.arange(0, 300, 3)
+    ref_o, ref_l, _ = bench.oracle_sample(q, k, v, rows, kv_chunk=64, workers=1)
+    monkeypatch.setattr(bench, "CPU_SAMPLE_FLOP", 4 * 3 * 16 * 300 * 10)
+    seconds, timed, agree = bench.torch_cpu_sample(q[torch.from_numpy(rows)], k, v, 64, 1, ref_o, ref_l)
+    assert timed == 10 and seconds > 0
+    assert agree["max_abs_o"] < 1e-5 and agree["max_abs_lse"] < 1e-5
 
 
 @pytest.mark.parametrize("mistake", ["o_element", "lse_row", "row_swap", "head_swap"])
