@@ -123,6 +123,37 @@ def test_head_groups_repeated_runs_reuse_the_sets():
     check(small[0], small[1], ref_o, ref_l)
 
 
+def test_auto_schedule_runs_head_groups_or_q_blocks_with_the_same_bits():
+    """schedule="auto": head groups where a unit fits the budget (page-locked
+    inputs), Q blocks with pageable inputs allowed; both give the bits of an
+    explicit Q-block run at the same K/V chunk."""
+    announce("auto schedule")
+    gen = torch.Generator().manual_seed(73)
+    q = pinned_randn((1500, 6, 128), torch.bfloat16, gen)
+    k = pinned_randn((1400, 6, 128), torch.bfloat16, gen)
+    v = pinned_randn((1400, 6, 128), torch.bfloat16, gen)
+    cu_q = torch.tensor([0, 400, 1500], dtype=torch.int32)
+    cu_k = torch.tensor([0, 300, 1400], dtype=torch.int32)
+    shape = dict(q_heads=6, kv_heads=6, head_dim=128, dtype=torch.bfloat16, device="cuda", max_q_tokens=1500,
+                 max_kv_tokens=1400)
+    results = {}
+    for name, extra in (("q_blocks", {}), ("auto", {"schedule": "auto"}),
+                        ("auto_pageable", {"schedule": "auto", "require_pinned": False})):
+        config = StreamingAttentionConfig(backend="hip", kv_chunk_tokens=512, workspace_budget_bytes=40 * 2**20,
+                                          **extra)
+        plan = build_plan(config=config, **shape)
+        expected = "head_groups" if name == "auto" else "q_blocks"
+        assert plan.schedule == expected, name
+        inputs = (q, k, v) if name != "auto_pageable" else (q.clone(), k.clone(), v.clone())
+        out, lse, _ = run_plan(plan, config, *inputs, cu_q, cu_k, True)
+        results[name] = (out, lse)
+    for name in ("auto", "auto_pageable"):
+        torch.testing.assert_close(results[name][0], results["q_blocks"][0], atol=0, rtol=0)
+        torch.testing.assert_close(results[name][1], results["q_blocks"][1], atol=0, rtol=0)
+    ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=1500, kv_chunk=512, causal=True)
+    check(results["auto"][0], results["auto"][1], ref_o, ref_l)
+
+
 def test_head_groups_device_inputs_device_output_and_consumers():
     """On a head-group runner: device-resident inputs run the fused launch,
     and a device out is written by the unit launches (no output copy), both
