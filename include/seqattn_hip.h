@@ -209,7 +209,10 @@ int32_t sa_pipeline_create(
  *                sa_pipeline_attach_resident_scratch (used when a segment's
  *                group_kv_heads * 128 * roundup(keys, 64) * 2 bytes fit)
  *   num_sets     1 or 2; with 2, unit u uses set u % 2 and units alternate
- *                between compute_stream and a second stream of the pipeline
+ *                between compute_stream and a second stream of the pipeline,
+ *                and the units' sizes ramp up 1, 2, 4, ... K/V heads to
+ *                group_kv_heads (only the first unit's copies are exposed);
+ *                with 1, every unit but the last has group_kv_heads
  *   kv_chunk_tokens  where the row sums merge, as in a token-block pipeline of
  *                that K/V chunk, whose sa_pipeline_run output this matches bit
  *                for bit; a segment longer than one chunk needs a chunk that is

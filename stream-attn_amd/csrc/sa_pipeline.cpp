@@ -1008,8 +1008,8 @@ void scatter_rows(void* arg) {
   for (int64_t r = 0; r < s->rows; ++r) std::memcpy(s->dst + r * s->pitch, s->src + r * s->width, (size_t)s->width);
 }
 
-// sa_pipeline_run on a head-group pipeline.  Unit u (K/V heads
-// [u * group_kv, ...), with their query heads) uses buffer set u % num_sets
+// sa_pipeline_run on a head-group pipeline.  Unit u (a range of K/V heads,
+// at most group_kv, with their query heads) uses buffer set u % num_sets
 // and, with two sets, compute stream u % 2 (the caller's, then the
 // pipeline's second stream):
 //   H2D : [wait set_free] Q columns of every token, K and V columns (strided
@@ -1058,7 +1058,17 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
     return SA_ERR_INVALID_ARGUMENT;
   }
   const int64_t q_pitch = p->q_heads * d_bytes, kv_pitch = p->kv_heads * d_bytes;
-  const int units = (p->kv_heads + p->group_kv - 1) / p->group_kv;
+  // Units as K/V head ranges [kv0, kv0 + gk).  With two sets their sizes
+  // ramp up 1, 2, 4, ... to group_kv heads: the first unit's copies are the
+  // only ones no launch hides, so they are one head's.
+  std::vector<std::pair<int, int>> unit_list;
+  for (int kv0 = 0, size = p->num_sets > 1 ? 1 : p->group_kv; kv0 < p->kv_heads;) {
+    const int gk = std::min(std::min(size, p->group_kv), p->kv_heads - kv0);
+    unit_list.emplace_back(kv0, gk);
+    kv0 += gk;
+    size = std::min(2 * size, p->group_kv);
+  }
+  const int units = (int)unit_list.size();
   hipStream_t streams[sa_pipeline::kMaxSets] = {compute, p->side};
   SideJoin join{p, compute};
   if (p->num_sets > 1 && units > 1) {
@@ -1073,8 +1083,8 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
   std::vector<ScatterRows> scatters;
   if (p->staging != nullptr) {
     int64_t count = 0;
-    for (int u = 0; u < units; ++u) {
-      const int64_t wq = (int64_t)std::min(p->group_kv, p->kv_heads - u * p->group_kv) * group * d_bytes;
+    for (const auto& unit : unit_list) {
+      const int64_t wq = (int64_t)unit.second * group * d_bytes;
       count += (total_q + p->staging_bytes / wq - 1) / (p->staging_bytes / wq);
     }
     scatters.reserve((size_t)count);
@@ -1088,8 +1098,8 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
   // K/V heads [kv0, kv0 + gk) of unit u and the bytes of one row of its
   // Q/output (wq) and of its K and V (wk).
   auto unit_heads = [&](int u, int* kv0, int* gk, int64_t* wq, int64_t* wk) {
-    *kv0 = u * p->group_kv;
-    *gk = std::min(p->group_kv, p->kv_heads - *kv0);
+    *kv0 = unit_list[u].first;
+    *gk = unit_list[u].second;
     *wq = *gk * group * d_bytes;
     *wk = *gk * d_bytes;
   };

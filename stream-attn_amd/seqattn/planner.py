@@ -152,7 +152,23 @@ class AttentionPlan:
     @property
     def head_group_units(self) -> int:
         """Units of the head-group schedule (0 for the Q-block schedule)."""
-        return math.ceil(self.kv_heads / self.head_group_kv_heads) if self.head_group_kv_heads else 0
+        return len(head_group_unit_sizes(self.kv_heads, self.head_group_kv_heads, self.head_group_sets))
+
+
+def head_group_unit_sizes(kv_heads: int, group_kv: int, sets: int) -> list[int]:
+    """K/V heads of each unit of a head-group run, in order: with two buffer
+    sets the sizes ramp up 1, 2, 4, ... to ``group_kv`` (the first unit's
+    copies are the only ones no launch hides), with one set every unit but
+    the last has ``group_kv``.  The pipeline (sa_pipeline.cpp,
+    run_head_groups) splits the heads the same way."""
+    if group_kv <= 0:
+        return []
+    sizes, done, size = [], 0, 1 if sets > 1 else group_kv
+    while done < kv_heads:
+        sizes.append(min(size, group_kv, kv_heads - done))
+        done += sizes[-1]
+        size = min(2 * size, group_kv)
+    return sizes
 
 
 def estimate_workspace_bytes(
@@ -318,14 +334,17 @@ def modeled_head_groups(*, max_q_tokens: int, max_kv_tokens: int, q_heads: int, 
     copies and the last unit's output copy are exposed, with one set every
     unit's copies are."""
     element = _element_size(dtype)
-    units = math.ceil(kv_heads / group_kv_heads)
+    sizes = head_group_unit_sizes(kv_heads, group_kv_heads, sets)
     h2d = (max_q_tokens * q_heads + 2 * max_kv_tokens * kv_heads) * head_dim * element
     d2h = max_q_tokens * q_heads * head_dim * element
     kernel = 4.0 * q_heads * head_dim * max_q_tokens * max_kv_tokens / rates.update_flops_per_second
     copy_in = h2d / rates.h2d_bytes_per_second
     copy_out = d2h / rates.h2d_bytes_per_second
-    exposed = (copy_in + copy_out) / units if sets > 1 else copy_in + copy_out
-    seconds = kernel + exposed + units * rates.launch_seconds
+    if sets > 1:
+        exposed = (copy_in * sizes[0] + copy_out * sizes[-1]) / kv_heads
+    else:
+        exposed = copy_in + copy_out
+    seconds = kernel + exposed + len(sizes) * rates.launch_seconds
     return seconds, copy_in / seconds
 
 
@@ -555,6 +574,7 @@ __all__ = [
     "estimate_workspace_bytes",
     "head_group_set_bytes",
     "measure_planner_rates",
+    "head_group_unit_sizes",
     "modeled_head_groups",
     "modeled_run",
 ]

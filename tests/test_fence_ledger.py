@@ -26,6 +26,7 @@ from pathlib import Path
 import pytest
 
 from seqattn import _native
+from seqattn.planner import head_group_unit_sizes
 
 ROOT = Path(__file__).resolve().parents[1]
 HEAD_BYTES = 2  # bf16
@@ -340,7 +341,7 @@ def test_head_group_schedule_is_race_free(ledger, num_sets, causal, heads):
         ledger.ledger_reset()
         stats = run_head_groups(ledger, num_sets=num_sets, causal=causal, q_lengths=q_lengths, k_lengths=k_lengths,
                                 group_kv=group_kv, q_heads=q_heads, kv_heads=kv_heads)
-        units = -(-kv_heads // group_kv)
+        units = len(head_group_unit_sizes(kv_heads, group_kv, num_sets))
         row = q_heads * 64 * HEAD_BYTES
         # Every byte of Q, K and V crosses the link once; the output once.
         assert stats.h2d_bytes == sum(q_lengths) * row + 2 * sum(k_lengths) * kv_heads * 64 * HEAD_BYTES

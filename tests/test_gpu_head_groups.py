@@ -20,6 +20,7 @@ import pytest
 import torch
 
 from seqattn import StreamingAttentionConfig, StreamingAttentionRunner, StreamingAttentionStats, build_plan
+from seqattn.planner import head_group_unit_sizes
 from test_gpu_streaming import announce, check, oracle, pinned_randn
 
 pytestmark = pytest.mark.gpu
@@ -83,7 +84,7 @@ def test_head_groups_bit_identical_to_q_blocks(case, causal):
     element = q.element_size()
     assert st_h.h2d_bytes == (q.numel() + k.numel() + v.numel()) * element
     assert st_h.d2h_bytes == st_b.d2h_bytes == q.numel() * element
-    assert st_h.q_chunks == -(-kv_heads // group_kv)
+    assert st_h.q_chunks == plan.head_group_units == len(head_group_unit_sizes(kv_heads, group_kv, sets))
     assert st_h.max_resident_q_tokens == 2500
     ref_o, ref_l = oracle(q, k, v, cu_q, cu_k, q_chunk=512, kv_chunk=256, causal=causal)
     check(out_h, lse_h, ref_o, ref_l)
@@ -98,13 +99,14 @@ def test_head_groups_repeated_runs_reuse_the_sets():
     q = pinned_randn((1500, 6, 128), torch.bfloat16, gen)
     k = pinned_randn((1400, 6, 128), torch.bfloat16, gen)
     v = pinned_randn((1400, 6, 128), torch.bfloat16, gen)
-    # 40 MiB: the fixed 32 MiB margin plus two sets of two K/V heads (three units).
+    # 40 MiB: the fixed 32 MiB margin plus two sets of two K/V heads; the
+    # units ramp up from one head: 1, 2, 2, 1.
     config = StreamingAttentionConfig(backend="hip", kv_chunk_tokens=512, schedule="head_groups",
                                       workspace_budget_bytes=40 * 2**20)
     plan = build_plan(q_heads=6, kv_heads=6, head_dim=128, dtype=torch.bfloat16, device="cuda",
                       max_q_tokens=1500, max_kv_tokens=1400, config=config)
     assert (plan.schedule, plan.head_group_sets, plan.head_group_kv_heads, plan.head_group_units) == (
-        "head_groups", 2, 2, 3)
+        "head_groups", 2, 2, 4)
     runner = StreamingAttentionRunner(plan, config)
     try:
         cu_q = torch.tensor([0, 1500], dtype=torch.int32)

@@ -9,7 +9,7 @@ import pytest
 import torch
 
 from seqattn import StreamingAttentionConfig, build_plan
-from seqattn.planner import estimate_workspace_bytes
+from seqattn.planner import estimate_workspace_bytes, head_group_unit_sizes
 
 GOLDEN = json.loads((Path(__file__).parent / "golden" / "planner_reference_rows.json").read_text())
 
@@ -212,9 +212,14 @@ def test_head_group_plan_drops_the_transposed_copy_before_the_second_set():
 
 def test_head_group_units_are_evened_out():
     # 14 GiB fits 12 heads per set pair (12 x 1.07 GB = 12.9 GB); 56 heads in
-    # ceil(56 / 12) = 5 units, evened out to ceil(56 / 5) = 12 per unit.
+    # ceil(56 / 12) = 5 units, evened out to ceil(56 / 5) = 12 per unit.  The
+    # run ramps the unit sizes up from one head (only the first unit's copies
+    # are exposed): 1, 2, 4, 8, 12, 12, 12 and the remaining 5.
     plan = _hg(14)
-    assert (plan.head_group_kv_heads, plan.head_group_units) == (12, 5)
+    assert (plan.head_group_kv_heads, plan.head_group_units) == (12, 8)
+    assert head_group_unit_sizes(56, 12, 2) == [1, 2, 4, 8, 12, 12, 12, 5]
+    # One set: no copy overlaps a launch, so no ramp.
+    assert head_group_unit_sizes(56, 12, 1) == [12, 12, 12, 12, 8]
     # GQA: a unit takes its K/V heads' query heads too (8 query heads per
     # K/V head here), and the transposed copy is per K/V head.
     plan = _hg(2, heads=64, kv_heads=8)
@@ -229,7 +234,7 @@ def test_head_group_plan_without_budget_holds_every_head_and_rejects_tiny_budget
     plan = build_plan(q_heads=8, kv_heads=2, head_dim=64, dtype=torch.bfloat16, device="cpu", max_q_tokens=4096,
                       max_kv_tokens=4096, config=StreamingAttentionConfig(schedule="head_groups"))
     assert (plan.head_group_sets, plan.head_group_kv_heads, plan.head_group_units, plan.head_group_vt_bytes) == (
-        2, 2, 1, 0)
+        2, 2, 2, 0)
     with pytest.raises(ValueError, match="too small for the head-group schedule"):
         _hg(0.25)
 
