@@ -1012,8 +1012,9 @@ void scatter_rows(void* arg) {
 // at most group_kv, with their query heads) uses buffer set u % num_sets
 // and, with two sets, compute stream u % 2 (the caller's, then the
 // pipeline's second stream):
-//   H2D : [wait set_free] Q columns of every token, K and V columns (strided
-//         copies from the host's [token][head][d] rows), record set_ready;
+//   H2D : [wait set_done] K and V columns of every token, [wait set_free] Q
+//         columns (strided copies from the host's [token][head][d] rows),
+//         record set_ready;
 //   compute: wait set_ready; per segment [transpose V], one fused update
 //         launch over all its queries and keys that writes the output (over
 //         the unit's Q rows) and the LSE; record set_done;
@@ -1113,17 +1114,21 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
     char* qo = static_cast<char*>(p->set_qo[b]);
     char* kd = static_cast<char*>(p->set_k[b]);
     char* vd = static_cast<char*>(p->set_v[b]);
+    // The set's K and V are free once its previous unit's launches have
+    // ended; its Q/output buffer only once that unit's output has left.  K
+    // and V go first, so that they land while that output is copied out.
+    {
+      TraceRange range(p->trace, "seqattn:kv_h2d");
+      if (p->set_pending[b]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->set_done[b], 0));
+      int32_t rc = copy_rows(kd, wk, kh + kv0 * d_bytes, kv_pitch, wk, total_k, hipMemcpyHostToDevice, p->h2d);
+      if (rc == 0) rc = copy_rows(vd, wk, vh + kv0 * d_bytes, kv_pitch, wk, total_k, hipMemcpyHostToDevice, p->h2d);
+      if (rc != 0) return rc;
+    }
     {
       TraceRange range(p->trace, "seqattn:q_h2d");
       if (p->set_pending[b]) SA_HIP_RETURN(hipStreamWaitEvent(p->h2d, p->set_free[b], 0));
       int32_t rc = copy_rows(qo, wq, qh + (int64_t)kv0 * group * d_bytes, q_pitch, wq, total_q,
                              hipMemcpyHostToDevice, p->h2d);
-      if (rc != 0) return rc;
-    }
-    {
-      TraceRange range(p->trace, "seqattn:kv_h2d");
-      int32_t rc = copy_rows(kd, wk, kh + kv0 * d_bytes, kv_pitch, wk, total_k, hipMemcpyHostToDevice, p->h2d);
-      if (rc == 0) rc = copy_rows(vd, wk, vh + kv0 * d_bytes, kv_pitch, wk, total_k, hipMemcpyHostToDevice, p->h2d);
       if (rc != 0) return rc;
       SA_HIP_RETURN(hipEventRecord(p->set_ready[b], p->h2d));
     }
