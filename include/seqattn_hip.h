@@ -220,7 +220,8 @@ int32_t sa_pipeline_create(
  *   h2d_stream, d2h_stream  as for sa_pipeline_create
  * Buffers are contiguous and 16-byte aligned.  sa_pipeline_run on such a
  * pipeline runs the head-group schedule: per unit, strided H2D copies of its
- * Q, K and V columns of every token (after the set's previous output copy),
+ * K and V columns of every token (after the set's previous launches) and of
+ * its Q columns (after the set's previous output copy),
  * one fused update launch per segment writing the output over the unit's Q
  * rows and the LSE, and a strided D2H of the output columns.  Inputs may
  * hold at most max_q_tokens / max_kv_tokens rows.  The step API
