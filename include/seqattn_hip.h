@@ -210,9 +210,11 @@ int32_t sa_pipeline_create(
  *                group_kv_heads * 128 * roundup(keys, 64) * 2 bytes fit)
  *   num_sets     1 or 2; with 2, unit u uses set u % 2 and units alternate
  *                between compute_stream and a second stream of the pipeline,
- *                and the units' sizes ramp up 1, 2, 4, ... K/V heads to
- *                group_kv_heads (only the first unit's copies are exposed);
- *                with 1, every unit but the last has group_kv_heads
+ *                and the units' sizes ramp up 1, 2, 4, ... K/V heads and back
+ *                down at the end, with units of at most group_kv_heads,
+ *                evened out, between (the first unit's copies and the last
+ *                units' output copies are the exposed ones); with 1, units
+ *                of at most group_kv_heads, evened out
  *   kv_chunk_tokens  where the row sums merge, as in a token-block pipeline of
  *                that K/V chunk, whose sa_pipeline_run output this matches bit
  *                for bit; a segment longer than one chunk needs a chunk that is

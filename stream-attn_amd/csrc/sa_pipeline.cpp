@@ -1008,6 +1008,38 @@ void scatter_rows(void* arg) {
   for (int64_t r = 0; r < s->rows; ++r) std::memcpy(s->dst + r * s->pitch, s->src + r * s->width, (size_t)s->width);
 }
 
+// K/V heads of each unit of a head-group run.  With two sets the sizes ramp
+// up 1, 2, 4, ... below group_kv and back down ..., 4, 2, 1 at the end, with
+// units of at most group_kv heads, evened out, between: the first unit's
+// copies and the last units' output copies are the only ones no launch
+// hides (the last two units' launches end together), so they are small.
+// With one set (nothing overlaps) every unit but the last has group_kv.
+std::vector<int> head_group_unit_sizes(int kv_heads, int group_kv, int num_sets) {
+  std::vector<int> sizes;
+  if (group_kv <= 0 || kv_heads <= 0) return sizes;
+  std::vector<int> ramp;
+  if (num_sets > 1)
+    for (int size = 1; size < group_kv; size *= 2) ramp.push_back(size);
+  int ramp_heads = 0;
+  for (const int size : ramp) ramp_heads += size;
+  if (2 * ramp_heads > kv_heads) {
+    // Too few heads for both ramps: ramp up only, then group_kv.
+    for (int done = 0, size = num_sets > 1 ? 1 : group_kv; done < kv_heads;) {
+      const int gk = std::min(std::min(size, group_kv), kv_heads - done);
+      sizes.push_back(gk);
+      done += gk;
+      size = std::min(2 * size, group_kv);
+    }
+    return sizes;
+  }
+  sizes = ramp;
+  const int middle = kv_heads - 2 * ramp_heads;
+  const int count = (middle + group_kv - 1) / group_kv;
+  for (int i = 0; i < count; ++i) sizes.push_back(middle / count + (i < middle % count ? 1 : 0));
+  sizes.insert(sizes.end(), ramp.rbegin(), ramp.rend());
+  return sizes;
+}
+
 // sa_pipeline_run on a head-group pipeline.  Unit u (a range of K/V heads,
 // at most group_kv, with their query heads) uses buffer set u % num_sets
 // and, with two sets, compute stream u % 2 (the caller's, then the
@@ -1059,15 +1091,15 @@ int32_t run_head_groups(sa_pipeline* p, const char* qh, const char* kh, const ch
     return SA_ERR_INVALID_ARGUMENT;
   }
   const int64_t q_pitch = p->q_heads * d_bytes, kv_pitch = p->kv_heads * d_bytes;
-  // Units as K/V head ranges [kv0, kv0 + gk).  With two sets their sizes
-  // ramp up 1, 2, 4, ... to group_kv heads: the first unit's copies are the
-  // only ones no launch hides, so they are one head's.
+  // Units as K/V head ranges [kv0, kv0 + gk).
   std::vector<std::pair<int, int>> unit_list;
-  for (int kv0 = 0, size = p->num_sets > 1 ? 1 : p->group_kv; kv0 < p->kv_heads;) {
-    const int gk = std::min(std::min(size, p->group_kv), p->kv_heads - kv0);
-    unit_list.emplace_back(kv0, gk);
-    kv0 += gk;
-    size = std::min(2 * size, p->group_kv);
+  {
+    const std::vector<int> sizes = head_group_unit_sizes(p->kv_heads, p->group_kv, p->num_sets);
+    int kv0 = 0;
+    for (const int gk : sizes) {
+      unit_list.emplace_back(kv0, gk);
+      kv0 += gk;
+    }
   }
   const int units = (int)unit_list.size();
   hipStream_t streams[sa_pipeline::kMaxSets] = {compute, p->side};

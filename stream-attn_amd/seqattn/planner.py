@@ -156,19 +156,33 @@ class AttentionPlan:
 
 
 def head_group_unit_sizes(kv_heads: int, group_kv: int, sets: int) -> list[int]:
-    """K/V heads of each unit of a head-group run, in order: with two buffer
-    sets the sizes ramp up 1, 2, 4, ... to ``group_kv`` (the first unit's
-    copies are the only ones no launch hides), with one set every unit but
-    the last has ``group_kv``.  The pipeline (sa_pipeline.cpp,
-    run_head_groups) splits the heads the same way."""
-    if group_kv <= 0:
+    """K/V heads of each unit of a head-group run, in order.  With two buffer
+    sets the sizes ramp up 1, 2, 4, ... below ``group_kv`` and back down
+    ..., 4, 2, 1 at the end, with units of at most ``group_kv`` heads,
+    evened out, between: the first unit's copies and the last units' output
+    copies are the only ones no launch hides.  Too few heads for both ramps:
+    the ramp up, then ``group_kv``.  With one set, units of at most
+    ``group_kv``, evened out.  The pipeline (sa_pipeline.cpp,
+    head_group_unit_sizes) splits the heads the same way."""
+    if group_kv <= 0 or kv_heads <= 0:
         return []
-    sizes, done, size = [], 0, 1 if sets > 1 else group_kv
-    while done < kv_heads:
-        sizes.append(min(size, group_kv, kv_heads - done))
-        done += sizes[-1]
-        size = min(2 * size, group_kv)
-    return sizes
+    ramp = []
+    if sets > 1:
+        size = 1
+        while size < group_kv:
+            ramp.append(size)
+            size *= 2
+    if 2 * sum(ramp) > kv_heads:
+        sizes, done, size = [], 0, 1 if sets > 1 else group_kv
+        while done < kv_heads:
+            sizes.append(min(size, group_kv, kv_heads - done))
+            done += sizes[-1]
+            size = min(2 * size, group_kv)
+        return sizes
+    middle = kv_heads - 2 * sum(ramp)
+    count = -(-middle // group_kv)
+    even = [middle // count + (1 if i < middle % count else 0) for i in range(count)] if count else []
+    return ramp + even + ramp[::-1]
 
 
 def estimate_workspace_bytes(

@@ -171,14 +171,14 @@ def test_config5_1m_64h_peaked_keys_8gib_workspace():
     idx = torch.from_numpy(rows)
     o_rows, l_rows = out[idx].clone(), lse[:, idx.cuda()].cpu()
     check_parity(o_rows.float().numpy(), l_rows.numpy(), ref_o, ref_l, f"{rows.size} rows x {h} heads")
-    # The same step in the head-group schedule (23 units of up to 3 K/V heads; a
+    # The same step in the head-group schedule (24 units of up to 3 K/V heads; a
     # pageable output goes through the pipeline's page-locked staging):
     # the same bits on the sampled rows.
     hg_config = StreamingAttentionConfig(workspace_budget_bytes=8 * 2**30, kv_chunk_tokens=8192, backend="hip",
                                          pin_output=out.is_pinned(), schedule="head_groups")
     hg_plan = build_plan(q_heads=h, kv_heads=h, head_dim=d, dtype=torch.bfloat16, device="cuda",
                          max_q_tokens=n, max_kv_tokens=n, config=hg_config)
-    assert (hg_plan.head_group_sets, hg_plan.head_group_kv_heads, hg_plan.head_group_units) == (2, 3, 23)
+    assert (hg_plan.head_group_sets, hg_plan.head_group_kv_heads, hg_plan.head_group_units) == (2, 3, 24)
     runner = StreamingAttentionRunner(hg_plan, hg_config)
     out.fill_(float("nan"))
     lse.fill_(float("nan"))

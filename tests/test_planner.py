@@ -213,13 +213,17 @@ def test_head_group_plan_drops_the_transposed_copy_before_the_second_set():
 def test_head_group_units_are_evened_out():
     # 14 GiB fits 12 heads per set pair (12 x 1.07 GB = 12.9 GB); 56 heads in
     # ceil(56 / 12) = 5 units, evened out to ceil(56 / 5) = 12 per unit.  The
-    # run ramps the unit sizes up from one head (only the first unit's copies
-    # are exposed): 1, 2, 4, 8, 12, 12, 12 and the remaining 5.
+    # run ramps the unit sizes up from one head and back down to one (only
+    # the first unit's copies and the last units' output copies are
+    # exposed), with the 42 heads between in units of at most 12, evened out.
     plan = _hg(14)
-    assert (plan.head_group_kv_heads, plan.head_group_units) == (12, 8)
-    assert head_group_unit_sizes(56, 12, 2) == [1, 2, 4, 8, 12, 12, 12, 5]
-    # One set: no copy overlaps a launch, so no ramp.
-    assert head_group_unit_sizes(56, 12, 1) == [12, 12, 12, 12, 8]
+    assert (plan.head_group_kv_heads, plan.head_group_units) == (12, 11)
+    assert head_group_unit_sizes(56, 12, 2) == [1, 2, 4, 8, 9, 9, 8, 8, 4, 2, 1]
+    # Too few heads for both ramps: up only.  One set (no copy overlaps a
+    # launch): no ramp.
+    assert head_group_unit_sizes(8, 8, 2) == [1, 2, 4, 1]
+    assert head_group_unit_sizes(56, 12, 1) == [12, 11, 11, 11, 11]
+    assert head_group_unit_sizes(56, 1, 2) == [1] * 56
     # GQA: a unit takes its K/V heads' query heads too (8 query heads per
     # K/V head here), and the transposed copy is per K/V head.
     plan = _hg(2, heads=64, kv_heads=8)
