@@ -236,6 +236,7 @@ def test_device_resident_inputs_are_bit_identical_to_streamed(causal, kv_chunk):
     (torch.bfloat16, 64, 6, 2),
     (torch.bfloat16, 96, 4, 1),
     (torch.bfloat16, 256, 2, 1),
+    (torch.bfloat16, 128, 12, 4),  # causal blocks dealt to XCDs in a launch of more than 8 heads
 ])
 def test_fused_resident_launch_matches_streamed_at_every_geometry(dtype, head_dim, q_heads, kv_heads):
     """With device inputs and a K/V chunk that is a multiple of 64, each
