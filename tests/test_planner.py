@@ -286,3 +286,15 @@ def test_auto_schedule_plans_head_groups_when_they_fit():
     # move by strided copies from them, so Q blocks.
     pageable = StreamingAttentionConfig(workspace_budget_bytes=2 * 2**30, schedule="auto", require_pinned=False)
     assert build_plan(config=pageable, **shape).schedule == "q_blocks"
+
+
+def test_head_group_unit_sizes_cover_every_head_within_the_group_size():
+    for kv_heads in range(1, 65):
+        for group_kv in range(1, 17):
+            for sets in (1, 2):
+                sizes = head_group_unit_sizes(kv_heads, group_kv, sets)
+                assert sum(sizes) == kv_heads and all(1 <= s <= group_kv for s in sizes)
+                if sets == 2:
+                    assert sizes[0] == 1
+                else:
+                    assert len(sizes) == -(-kv_heads // group_kv)
